@@ -1,0 +1,186 @@
+/*
+ * libipus: C ABI of the MI355X (gfx950) backend for the ipu-stack hot path.
+ *
+ * This header is the drop-in boundary.  It replaces the roles that the
+ * reference splits over four Rust crates:
+ *   - ipu-runtime / ipu-driver (device open, host sessions, PCIe exchange):
+ *       crates/ipu-runtime/src/lib.rs:17-47, crates/ipu-driver/src/lib.rs:1341-1600
+ *     -> ipus_context_*, ipus_buffer_*, ipus_stream_sync, ipus_event_*
+ *   - ipu-elf (compile + link, symbol lookup): crates/ipu-elf/src/lib.rs:86-170, 322
+ *     -> kernels are compiled into this library; ipus_kernel_abi looks them up
+ *   - ipu-target (ComputeStep emission: m2 = output, m3.. = inputs, then u32
+ *     scalars): crates/ipu-target/src/program.rs:112-121,
+ *     crates/ipu-target/src/emit.rs:514-551,
+ *     crates/ipu-codegen/src/kernel.rs:14-16, 818-865
+ *     -> ipus_launch(symbol, out, inputs, scalars)
+ *   - the tile-kernel ABI registry and run validation:
+ *     crates/ipu-codegen/src/kernel.rs:1215-1435 (tile_kernel_abi,
+ *     validate_kernel_run) -> ipus_kernel_abi + the checks inside ipus_launch.
+ *
+ * Conventions (kernel.rs:14-16, crates/ipu-codegen/src/operator.rs:467-537):
+ *   - The caller owns every buffer.  Kernels read inputs and write the output
+ *     and allocate nothing (the row reduction's partial sums use a per-context
+ *     workspace that the context owns).
+ *   - Launches are ordered on the context's stream (replacing BSP phases).
+ *   - Every call returns 0 on success or a negative IPUS_ERROR_* code;
+ *     ipus_last_error() returns the message of the calling thread's last
+ *     failure.  HIP runtime failures map to IPUS_ERROR_HIP_BASE - hipError_t.
+ *   - Scalars are u32, as in the reference's PlannedKernelCall::arguments
+ *     (kernel.rs:136-140).  f32 values travel as their bit patterns, as in
+ *     AttentionScale::ValueBits (crates/ipu-codegen/src/graph.rs:147-165).
+ */
+#ifndef IPUS_H
+#define IPUS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (KernelAbiError, kernel.rs:140-162) ---- */
+#define IPUS_OK 0
+#define IPUS_ERROR_INVALID_ARGUMENT (-1)   /* RequirementMismatch / bad shape */
+#define IPUS_ERROR_POINTER_ARITY (-2)      /* PointerArity { expected, actual } */
+#define IPUS_ERROR_UNAVAILABLE (-3)        /* Unavailable(spec): no device kernel */
+#define IPUS_ERROR_UNSUPPORTED_COUNT (-4)  /* UnsupportedElementCount */
+#define IPUS_ERROR_UNKNOWN_SYMBOL (-5)     /* symbol not in the registry */
+#define IPUS_ERROR_GRAPH (-6)              /* GraphError (graph.rs:221-245) */
+#define IPUS_ERROR_BUILD (-7)              /* PackageBuildError (package.rs:48-78) */
+#define IPUS_ERROR_NO_DEVICE (-8)
+#define IPUS_ERROR_OUT_OF_MEMORY (-9)
+#define IPUS_ERROR_HIP_BASE (-1000)        /* IPUS_ERROR_HIP_BASE - hipError_t */
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char *ipus_last_error(void);
+/* Library version string. */
+const char *ipus_version(void);
+
+/* ---- context: one device, one stream (Runtime::open / HostSession) ---- */
+typedef struct ipus_context ipus_context;
+
+typedef struct ipus_device_info {
+  char name[64];          /* e.g. "AMD Instinct MI355X" */
+  char arch[32];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int compute_units;
+  int clock_khz;
+  int memory_clock_khz;
+  int memory_bus_width;
+  uint64_t global_memory_bytes;
+  int lds_bytes_per_block;
+} ipus_device_info;
+
+int ipus_device_count(int *count);
+int ipus_context_create(int device, ipus_context **out);
+int ipus_context_destroy(ipus_context *context);
+int ipus_context_device_info(ipus_context *context, ipus_device_info *info);
+/* Stream handle (hipStream_t) of the context, for callers that interoperate
+ * with other HIP code.  Launches through this library go to this stream. */
+int ipus_context_stream(ipus_context *context, void **stream);
+
+/* ---- buffers: replace SRAM placement, host exchange and FillZero ---- */
+int ipus_buffer_alloc(ipus_context *context, size_t bytes, void **device_pointer);
+int ipus_buffer_free(ipus_context *context, void *device_pointer);
+/* Synchronous host <-> device copies (complete before returning). */
+int ipus_buffer_upload(ipus_context *context, void *device_dst, const void *host_src,
+                       size_t bytes);
+int ipus_buffer_download(ipus_context *context, void *host_dst, const void *device_src,
+                         size_t bytes);
+/* Stream-ordered device copy and byte fill. */
+int ipus_buffer_copy(ipus_context *context, void *device_dst, const void *device_src,
+                     size_t bytes);
+int ipus_buffer_memset(ipus_context *context, void *device_pointer, int value, size_t bytes);
+
+/* ---- synchronisation and timing ---- */
+int ipus_stream_sync(ipus_context *context);
+typedef struct ipus_event ipus_event;
+int ipus_event_create(ipus_context *context, ipus_event **event);
+int ipus_event_destroy(ipus_event *event);
+int ipus_event_record(ipus_context *context, ipus_event *event);
+int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *milliseconds);
+
+/* ---- kernel ABI registry (tile_kernel_abi, kernel.rs:1215-1382) ----
+ *
+ * Symbols (output, inputs, u32 scalars in order):
+ *   ipu_stack_gemm_f16                 out f16 [B,M,N]; left, right f16;
+ *        batches, rows, columns, inner, transpose_left, transpose_right,
+ *        left_batch_stride, right_batch_stride  (strides in elements, 0 =
+ *        broadcast).  Replaces gemm_f16_amp (device/gemm_f16_amp.S:186-440)
+ *        with fp32 accumulation and fp16 output.
+ *   ipu_stack_gemm_f32                 as above in fp32
+ *        (device/gemm_f32_64_amp.S:125-385).
+ *   ipu_stack_flash_attention_online_f16  out (f32 or f16); query, key,
+ *        value f16 [streams, rows, width]; matrices, query_rows, key_rows,
+ *        query_dimension, value_dimension, scale_bits (0 = 1/sqrt(width)),
+ *        causal, output_f16.  Shape fields follow AttentionKernelShape
+ *        (kernel.rs:121-129); semantics device/flash_attention_online_f16.cpp:
+ *        68-143 plus the causal limit of crates/ipu-tests/src/diagnostic.rs:741-745.
+ *   ipu_stack_gelu_tanh_approx_f16     out f16; input f16; element_count
+ *        (kernel.rs:1251-1263; count must be even, kernel.rs:1400-1413).
+ *   ipu_stack_reduce_sum_f16           out f16; initial, packed remotes f16;
+ *        num_partials (= remote partial count), element_count
+ *        (kernel.rs:1264-1274; partials >= 2 and count % 8 == 0,
+ *        kernel.rs:1414-1423; semantics device/reduce_add_f16.S:54-70).
+ *   ipu_stack_rearrange_row_major_f16  out f16; source f16 row-major;
+ *        logical_rows, physical_rows, target_order (0 AmpLeft,
+ *        1 AmpTransposedRight, 2 BlockMajor), logical_columns,
+ *        physical_columns, row_block, column_block, matrices
+ *        (kernel.rs:1340-1364; device/rearrange_f16.cpp:36-155).
+ *   ipu_stack_unpack_amp_f16           out f16 row-major; source f16;
+ *        matrices, logical_rows, physical_rows, logical_columns,
+ *        physical_columns, source_order (0 AmpOutput, 1 AmpTransposedLeft)
+ *        (kernel.rs:1319-1339; device/unpack_amp_f16.cpp:30-83).
+ *   ipu_stack_transpose_f16            out f16 [B,N,M]; source f16 [B,M,N];
+ *        matrices, rows, columns.  No reference symbol: the graph-level
+ *        transpose of a row-major matrix (BlockMajorOrder::TransposedMatrix
+ *        semantics, crates/ipu-codegen/src/storage.rs:390-401).
+ *   ipu_stack_reduce_rows_f16          out f32 [rows]; source f16 logical
+ *        [rows, columns]; rows, columns, source_order (3 row-major,
+ *        2 block-major), row_block, column_block.  ReductionSum over the
+ *        columns with fp32 accumulation (operator.rs:307-347).
+ *   ipu_stack_fill_zero                out; no inputs; byte_count
+ *        (FillZero, kernel.rs:1231-1236).
+ *   ipu_stack_cast_f32_f16, ipu_stack_cast_f16_f32   out; input;
+ *        element_count (Cast, kernel.rs:1313-1318).
+ *   ipu_stack_add_f16, ipu_stack_add_f32   out; left, right; element_count,
+ *        left_broadcast_stride, right_broadcast_stride  (Add,
+ *        kernel.rs:1275-1287): out[i] = left[i % L] + right[i % R] where
+ *        L, R are the operand element counts given by the two strides
+ *        (trailing-axis numpy broadcasting; the graph executor handles the
+ *        general case).
+ */
+#define IPUS_MAX_SCALARS 32
+
+typedef struct ipus_kernel_abi_info {
+  const char *symbol;
+  int input_count;
+  int scalar_count;
+  const char *scalar_names[IPUS_MAX_SCALARS];
+  int implemented; /* KernelAvailability::Implemented */
+} ipus_kernel_abi_info;
+
+int ipus_kernel_count(int *count);
+int ipus_kernel_abi_at(int index, ipus_kernel_abi_info *info);
+int ipus_kernel_abi(const char *symbol, ipus_kernel_abi_info *info);
+
+/* One ComputeStep{symbol, output_address, input_addresses, arguments}:
+ * validates pointer arity and scalar constraints (validate_kernel_run,
+ * kernel.rs:1384-1435) and enqueues on the context stream. */
+int ipus_launch(ipus_context *context, const char *symbol, void *output,
+                const void *const *inputs, int input_count, const uint32_t *scalars,
+                int scalar_count);
+
+/* ---- synthetic inputs (host, deterministic, multithreaded) ----
+ * value(seed, tensor, i) from SplitMix64(seed ^ (tensor << 48) ^ i):
+ * distribution 0 = uniform [-1, 1) from the top 24 bits, 1 = normal (Box-Muller
+ * on two draws), times `scale`; fp16 outputs are rounded to nearest even. */
+int ipus_synth_f16(uint16_t *out, uint64_t count, uint64_t seed, uint32_t tensor,
+                   int distribution, float scale);
+int ipus_synth_f32(float *out, uint64_t count, uint64_t seed, uint32_t tensor,
+                   int distribution, float scale);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IPUS_H */

@@ -1,0 +1,153 @@
+/*
+ * libipus graph API: the ipu-codegen surface, build_package(ComputeGraph,
+ * PackageConfig), lowered to a plan of GPU kernel launches.
+ *
+ * Reference interface replaced, per entry point:
+ *   ComputeGraph (crates/ipu-codegen/src/graph.rs:209-515):
+ *     ipus_graph_host_input      graph.rs:278-284   ComputeGraph::host_input
+ *     ipus_graph_parameter       graph.rs:286-292   ComputeGraph::parameter
+ *     ipus_graph_value_sequence  graph.rs:294-313   ComputeGraph::value_sequence
+ *     ipus_graph_gemm            graph.rs:315-326   gemm / gemm_with_options
+ *     ipus_graph_gelu            graph.rs:328-330   gelu
+ *     ipus_graph_add             graph.rs:332-334   add (numpy broadcasting)
+ *     ipus_graph_split_heads     graph.rs:336-343   split_heads
+ *     ipus_graph_flash_attention graph.rs:345-362   flash_attention_with_options
+ *     ipus_graph_repeat_begin/_end graph.rs:382-472 repeat (closure body)
+ *     ipus_graph_set_outputs     graph.rs:474-479   set_outputs
+ *     ipus_graph_value_shape     graph.rs:270-272   value_shape
+ *   Graph-level extensions for the layout chain (no reference op: the
+ *   reference inserts rearranges during mid lowering, mid.rs:3553-3642):
+ *     ipus_graph_transpose, ipus_graph_rearrange, ipus_graph_reduce_rows
+ *   build_package (crates/ipu-codegen/src/package.rs:532-538):
+ *     ipus_build_package(graph, config) -> package (launch plan + bindings;
+ *     CompiledPackage, package.rs:108-145)
+ *   HostSession (crates/ipu-driver/src/lib.rs:1341-1600; invoke "run",
+ *   crates/ipu-tests/src/main.rs:1523-1561):
+ *     ipus_session_create / _write / _run / _read
+ *
+ * Errors: graph calls return IPUS_ERROR_GRAPH with the GraphError message
+ * (graph.rs:221-245) in ipus_last_error(); build errors return
+ * IPUS_ERROR_BUILD.
+ */
+#ifndef IPUS_GRAPH_H
+#define IPUS_GRAPH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ipus.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ipus_graph ipus_graph;
+typedef uint32_t ipus_value;    /* ValueId */
+typedef uint32_t ipus_sequence; /* ValueSequenceId */
+
+#define IPUS_MAX_RANK 8
+
+/* Precisions (crates/ipu-codegen/src/operator.rs:14-21). */
+#define IPUS_PRECISION_F16 1
+#define IPUS_PRECISION_F32 2
+
+/* Physical orders of a stored tensor (layout.rs:7-30 plus row-major). */
+#define IPUS_ORDER_AMP_LEFT 0
+#define IPUS_ORDER_AMP_TRANSPOSED_RIGHT 1
+#define IPUS_ORDER_BLOCK_MAJOR 2
+#define IPUS_ORDER_ROW_MAJOR 3
+
+int ipus_graph_create(ipus_graph **out);
+int ipus_graph_destroy(ipus_graph *graph);
+
+int ipus_graph_host_input(ipus_graph *graph, const char *name, const uint32_t *dims, int rank,
+                          ipus_value *out);
+int ipus_graph_parameter(ipus_graph *graph, const char *name, const uint32_t *dims, int rank,
+                         ipus_value *out);
+int ipus_graph_value_sequence(ipus_graph *graph, const char *name, const ipus_value *values,
+                              int count, ipus_sequence *out);
+int ipus_graph_gemm(ipus_graph *graph, ipus_value left, ipus_value right, int transpose_left,
+                    int transpose_right, ipus_value *out);
+int ipus_graph_gelu(ipus_graph *graph, ipus_value input, ipus_value *out);
+int ipus_graph_add(ipus_graph *graph, ipus_value left, ipus_value right, ipus_value *out);
+int ipus_graph_split_heads(ipus_graph *graph, ipus_value input, uint32_t heads, ipus_value *out);
+/* has_scale = 0: AttentionScale::InverseSqrtQueryWidth; otherwise
+ * AttentionScale::ValueBits(scale_bits) (must be finite and positive). */
+int ipus_graph_flash_attention(ipus_graph *graph, ipus_value query, ipus_value key,
+                               ipus_value value, int causal, int has_scale, uint32_t scale_bits,
+                               ipus_value *out);
+/* Extensions: logical transpose of the last two axes; a physical re-layout
+ * (same logical tensor, stored in `order`); row sums over the last axis with
+ * fp32 accumulation (result F32, shape without the last axis). */
+int ipus_graph_transpose(ipus_graph *graph, ipus_value input, ipus_value *out);
+int ipus_graph_rearrange(ipus_graph *graph, ipus_value input, int order, uint32_t row_block,
+                         uint32_t column_block, ipus_value *out);
+int ipus_graph_reduce_rows(ipus_graph *graph, ipus_value input, ipus_value *out);
+
+/* Structured repeat.  Between begin and end, graph calls add operations to
+ * the body region.  `arguments` receives carried, invariant then iterated
+ * argument values (RepeatArguments, graph.rs:196-201). */
+int ipus_graph_repeat_begin(ipus_graph *graph, uint32_t count, const ipus_value *carried,
+                            int carried_count, const ipus_value *invariants, int invariant_count,
+                            const ipus_sequence *iterated, int iterated_count,
+                            ipus_value *arguments);
+int ipus_graph_repeat_end(ipus_graph *graph, const ipus_value *yields, int yield_count,
+                          ipus_value *results);
+/* Discards the innermost open body (the closure returned an error). */
+int ipus_graph_repeat_abort(ipus_graph *graph);
+
+int ipus_graph_set_outputs(ipus_graph *graph, const ipus_value *values, int count);
+int ipus_graph_value_shape(const ipus_graph *graph, ipus_value value, uint32_t *dims,
+                           int capacity, int *rank);
+int ipus_graph_operation_count(const ipus_graph *graph, int *count);
+
+/* ---- package ---- */
+typedef struct ipus_package_config {
+  int compute_precision;    /* IPUS_PRECISION_F16 (default) or _F32 */
+  int attention_output_f16; /* 0: F32 attention output (reference), 1: F16 */
+} ipus_package_config;
+
+typedef struct ipus_package ipus_package;
+
+typedef struct ipus_tensor_info {
+  const char *name;
+  uint32_t value;
+  int rank;
+  uint32_t dims[IPUS_MAX_RANK];
+  int precision;
+  int order;
+  uint32_t row_block, column_block;
+  uint64_t bytes;
+} ipus_tensor_info;
+
+int ipus_build_package(const ipus_graph *graph, const ipus_package_config *config,
+                       ipus_package **out);
+int ipus_package_destroy(ipus_package *package);
+int ipus_package_input_count(const ipus_package *package, int *count);
+int ipus_package_input_info(const ipus_package *package, int index, ipus_tensor_info *info);
+int ipus_package_output_count(const ipus_package *package, int *count);
+int ipus_package_output_info(const ipus_package *package, int index, ipus_tensor_info *info);
+/* Launch plan inspection: one ComputeStep per entry. */
+int ipus_package_step_count(const ipus_package *package, int *count);
+int ipus_package_step(const ipus_package *package, int index, const char **symbol,
+                      int *input_count, int *scalar_count, const uint32_t **scalars);
+/* Bytes of the intermediate arena (lifetime-packed, replaces SRAM placement). */
+int ipus_package_arena_bytes(const ipus_package *package, uint64_t *bytes);
+/* Storage precision chosen for a graph value (CompiledPackage::precisions). */
+int ipus_package_value_precision(const ipus_package *package, ipus_value value, int *precision);
+
+/* ---- session: device buffers for one package ---- */
+typedef struct ipus_session ipus_session;
+int ipus_session_create(ipus_context *context, const ipus_package *package, ipus_session **out);
+int ipus_session_destroy(ipus_session *session);
+/* Binding names: the graph input names; outputs are "output.<i>". */
+int ipus_session_write(ipus_session *session, const char *name, const void *host, size_t bytes);
+int ipus_session_read(ipus_session *session, const char *name, void *host, size_t bytes);
+int ipus_session_tensor_pointer(ipus_session *session, const char *name, void **device_pointer);
+/* Enqueues every step on the context stream (asynchronous). */
+int ipus_session_run(ipus_session *session);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IPUS_GRAPH_H */

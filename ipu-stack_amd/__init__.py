@@ -1,0 +1,729 @@
+"""ipu-stack for MI355X: Python binding of libipus (ctypes over the C ABI).
+
+libipus.so (built in this directory by ``make``) holds the gfx950 kernels,
+the kernel ABI registry, the ComputeGraph / build_package compiler and the
+session executor; this module only marshals calls.  There is no CPU path:
+every function that computes goes through libipus on a HIP device, and the
+module raises if the library or the device is missing.
+
+The API mirrors the reference's ipu-codegen surface
+(crates/ipu-codegen/src/graph.rs:249-515, package.rs:532-538) in Python
+spelling: ``ComputeGraph``, ``build_package(graph, config)``, plus the
+kernel-level ``Context.launch`` that mirrors one ComputeStep
+(crates/ipu-codegen/src/kernel.rs:818-865).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+from dataclasses import dataclass, field
+from typing import Callable, Iterable, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(HERE, "libipus.so")
+
+PRECISION_F16 = 1
+PRECISION_F32 = 2
+ORDER_AMP_LEFT = 0
+ORDER_AMP_TRANSPOSED_RIGHT = 1
+ORDER_BLOCK_MAJOR = 2
+ORDER_ROW_MAJOR = 3
+
+OK = 0
+ERROR_INVALID_ARGUMENT = -1
+ERROR_POINTER_ARITY = -2
+ERROR_UNAVAILABLE = -3
+ERROR_UNSUPPORTED_COUNT = -4
+ERROR_UNKNOWN_SYMBOL = -5
+ERROR_GRAPH = -6
+ERROR_BUILD = -7
+ERROR_NO_DEVICE = -8
+ERROR_OUT_OF_MEMORY = -9
+ERROR_HIP_BASE = -1000
+
+MAX_RANK = 8
+MAX_SCALARS = 32
+
+
+class IpusError(RuntimeError):
+    """A libipus call failed; ``status`` is the negative IPUS_ERROR_* code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+        self.message = message
+
+
+class GraphError(IpusError):
+    """GraphError of crates/ipu-codegen/src/graph.rs:221-245."""
+
+
+class PackageBuildError(IpusError):
+    """PackageBuildError of crates/ipu-codegen/src/package.rs:48-78."""
+
+
+class KernelAbiError(IpusError):
+    """KernelAbiError of crates/ipu-codegen/src/kernel.rs:140-162."""
+
+
+class _KernelAbiInfo(ctypes.Structure):
+    _fields_ = [
+        ("symbol", ctypes.c_char_p),
+        ("input_count", ctypes.c_int),
+        ("scalar_count", ctypes.c_int),
+        ("scalar_names", ctypes.c_char_p * MAX_SCALARS),
+        ("implemented", ctypes.c_int),
+    ]
+
+
+class _DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 64),
+        ("arch", ctypes.c_char * 32),
+        ("compute_units", ctypes.c_int),
+        ("clock_khz", ctypes.c_int),
+        ("memory_clock_khz", ctypes.c_int),
+        ("memory_bus_width", ctypes.c_int),
+        ("global_memory_bytes", ctypes.c_uint64),
+        ("lds_bytes_per_block", ctypes.c_int),
+    ]
+
+
+class _TensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("value", ctypes.c_uint32),
+        ("rank", ctypes.c_int),
+        ("dims", ctypes.c_uint32 * MAX_RANK),
+        ("precision", ctypes.c_int),
+        ("order", ctypes.c_int),
+        ("row_block", ctypes.c_uint32),
+        ("column_block", ctypes.c_uint32),
+        ("bytes", ctypes.c_uint64),
+    ]
+
+
+class _PackageConfig(ctypes.Structure):
+    _fields_ = [("compute_precision", ctypes.c_int), ("attention_output_f16", ctypes.c_int)]
+
+
+_LIB: ctypes.CDLL | None = None
+
+_P = ctypes.c_void_p
+_U32P = ctypes.POINTER(ctypes.c_uint32)
+_SIGNATURES = {
+    "ipus_last_error": (ctypes.c_char_p, []),
+    "ipus_version": (ctypes.c_char_p, []),
+    "ipus_device_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
+    "ipus_context_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_P)]),
+    "ipus_context_destroy": (ctypes.c_int, [_P]),
+    "ipus_context_device_info": (ctypes.c_int, [_P, ctypes.POINTER(_DeviceInfo)]),
+    "ipus_context_stream": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "ipus_buffer_alloc": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.POINTER(_P)]),
+    "ipus_buffer_free": (ctypes.c_int, [_P, _P]),
+    "ipus_buffer_upload": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
+    "ipus_buffer_download": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
+    "ipus_buffer_copy": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
+    "ipus_buffer_memset": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_size_t]),
+    "ipus_stream_sync": (ctypes.c_int, [_P]),
+    "ipus_event_create": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "ipus_event_destroy": (ctypes.c_int, [_P]),
+    "ipus_event_record": (ctypes.c_int, [_P, _P]),
+    "ipus_event_elapsed_ms": (ctypes.c_int, [_P, _P, ctypes.POINTER(ctypes.c_float)]),
+    "ipus_kernel_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
+    "ipus_kernel_abi_at": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_KernelAbiInfo)]),
+    "ipus_kernel_abi": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_KernelAbiInfo)]),
+    "ipus_launch": (
+        ctypes.c_int,
+        [_P, ctypes.c_char_p, _P, ctypes.POINTER(_P), ctypes.c_int, _U32P, ctypes.c_int],
+    ),
+    "ipus_synth_f16": (
+        ctypes.c_int,
+        [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_float],
+    ),
+    "ipus_synth_f32": (
+        ctypes.c_int,
+        [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_float],
+    ),
+    "ipus_graph_create": (ctypes.c_int, [ctypes.POINTER(_P)]),
+    "ipus_graph_destroy": (ctypes.c_int, [_P]),
+    "ipus_graph_host_input": (ctypes.c_int, [_P, ctypes.c_char_p, _U32P, ctypes.c_int, _U32P]),
+    "ipus_graph_parameter": (ctypes.c_int, [_P, ctypes.c_char_p, _U32P, ctypes.c_int, _U32P]),
+    "ipus_graph_value_sequence": (
+        ctypes.c_int, [_P, ctypes.c_char_p, _U32P, ctypes.c_int, _U32P]),
+    "ipus_graph_gemm": (
+        ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, _U32P]),
+    "ipus_graph_gelu": (ctypes.c_int, [_P, ctypes.c_uint32, _U32P]),
+    "ipus_graph_add": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_uint32, _U32P]),
+    "ipus_graph_split_heads": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_uint32, _U32P]),
+    "ipus_graph_flash_attention": (
+        ctypes.c_int,
+        [_P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int,
+         ctypes.c_uint32, _U32P],
+    ),
+    "ipus_graph_transpose": (ctypes.c_int, [_P, ctypes.c_uint32, _U32P]),
+    "ipus_graph_rearrange": (
+        ctypes.c_int,
+        [_P, ctypes.c_uint32, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, _U32P],
+    ),
+    "ipus_graph_reduce_rows": (ctypes.c_int, [_P, ctypes.c_uint32, _U32P]),
+    "ipus_graph_repeat_begin": (
+        ctypes.c_int,
+        [_P, ctypes.c_uint32, _U32P, ctypes.c_int, _U32P, ctypes.c_int, _U32P, ctypes.c_int,
+         _U32P],
+    ),
+    "ipus_graph_repeat_end": (ctypes.c_int, [_P, _U32P, ctypes.c_int, _U32P]),
+    "ipus_graph_repeat_abort": (ctypes.c_int, [_P]),
+    "ipus_graph_set_outputs": (ctypes.c_int, [_P, _U32P, ctypes.c_int]),
+    "ipus_graph_value_shape": (
+        ctypes.c_int, [_P, ctypes.c_uint32, _U32P, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_graph_operation_count": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_build_package": (ctypes.c_int, [_P, ctypes.POINTER(_PackageConfig), ctypes.POINTER(_P)]),
+    "ipus_package_destroy": (ctypes.c_int, [_P]),
+    "ipus_package_input_count": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_package_input_info": (ctypes.c_int, [_P, ctypes.c_int, ctypes.POINTER(_TensorInfo)]),
+    "ipus_package_output_count": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_package_output_info": (ctypes.c_int, [_P, ctypes.c_int, ctypes.POINTER(_TensorInfo)]),
+    "ipus_package_step_count": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_package_step": (
+        ctypes.c_int,
+        [_P, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int),
+         ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_U32P)],
+    ),
+    "ipus_package_arena_bytes": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64)]),
+    "ipus_package_value_precision": (
+        ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(ctypes.c_int)]),
+    "ipus_session_create": (ctypes.c_int, [_P, _P, ctypes.POINTER(_P)]),
+    "ipus_session_destroy": (ctypes.c_int, [_P]),
+    "ipus_session_write": (ctypes.c_int, [_P, ctypes.c_char_p, _P, ctypes.c_size_t]),
+    "ipus_session_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, ctypes.c_size_t]),
+    "ipus_session_tensor_pointer": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "ipus_session_run": (ctypes.c_int, [_P]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Loads libipus.so (once) and declares every C signature.
+
+    Raises FileNotFoundError when the library has not been built: there is
+    no fallback implementation.
+    """
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    path = path or LIBRARY_PATH
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `make -C {HERE}` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path == LIBRARY_PATH:
+        _LIB = lib
+    return lib
+
+
+def _lib() -> ctypes.CDLL:
+    return _LIB if _LIB is not None else load_library()
+
+
+def last_error() -> str:
+    return (_lib().ipus_last_error() or b"").decode()
+
+
+def _check(status: int, kind: type = IpusError) -> None:
+    if status != 0:
+        if status == ERROR_GRAPH:
+            kind = GraphError
+        elif status == ERROR_BUILD:
+            kind = PackageBuildError
+        elif status in (ERROR_POINTER_ARITY, ERROR_UNAVAILABLE, ERROR_UNSUPPORTED_COUNT,
+                        ERROR_UNKNOWN_SYMBOL):
+            kind = KernelAbiError
+        raise kind(status, last_error())
+
+
+def _u32_array(values: Iterable[int]):
+    values = [int(v) for v in values]
+    return (ctypes.c_uint32 * max(1, len(values)))(*values), len(values)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(_lib().ipus_device_count(ctypes.byref(n)))
+    return n.value
+
+
+# ---------------------------------------------------------------------------
+# Kernel ABI registry
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class KernelAbi:
+    symbol: str
+    input_count: int
+    scalar_names: tuple
+    implemented: bool
+
+
+def _abi_from(info: _KernelAbiInfo) -> KernelAbi:
+    return KernelAbi(
+        info.symbol.decode(), info.input_count,
+        tuple(info.scalar_names[i].decode() for i in range(info.scalar_count)),
+        bool(info.implemented))
+
+
+def kernel_symbols() -> list[KernelAbi]:
+    n = ctypes.c_int(0)
+    _check(_lib().ipus_kernel_count(ctypes.byref(n)))
+    out = []
+    for i in range(n.value):
+        info = _KernelAbiInfo()
+        _check(_lib().ipus_kernel_abi_at(i, ctypes.byref(info)))
+        out.append(_abi_from(info))
+    return out
+
+
+def kernel_abi(symbol: str) -> KernelAbi:
+    info = _KernelAbiInfo()
+    _check(_lib().ipus_kernel_abi(symbol.encode(), ctypes.byref(info)))
+    return _abi_from(info)
+
+
+# ---------------------------------------------------------------------------
+# Synthetic inputs
+# ---------------------------------------------------------------------------
+UNIFORM = 0
+NORMAL = 1
+
+
+def synth_f16(count: int, seed: int, tensor: int, distribution: int = UNIFORM,
+              scale: float = 1.0) -> np.ndarray:
+    """fp16 bit patterns (uint16) of value(seed, tensor, i), i < count."""
+    out = np.empty(int(count), dtype=np.uint16)
+    _check(_lib().ipus_synth_f16(out.ctypes.data, int(count), int(seed), int(tensor),
+                                 int(distribution), float(scale)))
+    return out
+
+
+def synth_f32(count: int, seed: int, tensor: int, distribution: int = UNIFORM,
+              scale: float = 1.0) -> np.ndarray:
+    out = np.empty(int(count), dtype=np.float32)
+    _check(_lib().ipus_synth_f32(out.ctypes.data, int(count), int(seed), int(tensor),
+                                 int(distribution), float(scale)))
+    return out
+
+
+def _f32_bits(value: float) -> int:
+    return struct.unpack("<I", struct.pack("<f", float(value)))[0]
+
+
+def scale_bits(scale: float | None) -> int:
+    """Kernel-level scale scalar: AttentionScale::ValueBits (graph.rs:147-165),
+    0 = 1/sqrt(width) (a zero scale is never valid)."""
+    return 0 if scale is None else _f32_bits(scale)
+
+
+# ---------------------------------------------------------------------------
+# Device context, buffers, launches
+# ---------------------------------------------------------------------------
+class DeviceBuffer:
+    def __init__(self, context: "Context", ptr: int, nbytes: int):
+        self.context = context
+        self.ptr = ptr
+        self.nbytes = nbytes
+
+    def free(self) -> None:
+        if self.ptr:
+            _check(_lib().ipus_buffer_free(self.context.handle, self.ptr))
+            self.ptr = 0
+
+    def download(self, dtype, shape=None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        self.context.download_into(self, out)
+        return out.reshape(shape) if shape is not None else out
+
+
+class Context:
+    """One HIP device and stream (Runtime::open + HostSession roles)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        _check(_lib().ipus_context_create(int(device), ctypes.byref(h)))
+        self.handle = h.value
+        self._buffers: list[DeviceBuffer] = []
+
+    def close(self) -> None:
+        if self.handle:
+            for b in self._buffers:
+                if b.ptr:
+                    _lib().ipus_buffer_free(self.handle, b.ptr)
+                    b.ptr = 0
+            _lib().ipus_context_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def device_info(self) -> dict:
+        info = _DeviceInfo()
+        _check(_lib().ipus_context_device_info(self.handle, ctypes.byref(info)))
+        return {
+            "name": info.name.decode(), "arch": info.arch.decode(),
+            "compute_units": info.compute_units, "clock_khz": info.clock_khz,
+            "memory_clock_khz": info.memory_clock_khz,
+            "memory_bus_width": info.memory_bus_width,
+            "global_memory_bytes": info.global_memory_bytes,
+            "lds_bytes_per_block": info.lds_bytes_per_block,
+        }
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        p = ctypes.c_void_p()
+        _check(_lib().ipus_buffer_alloc(self.handle, int(nbytes), ctypes.byref(p)))
+        buf = DeviceBuffer(self, p.value, int(nbytes))
+        self._buffers.append(buf)
+        return buf
+
+    def upload(self, array: np.ndarray) -> DeviceBuffer:
+        array = np.ascontiguousarray(array)
+        buf = self.alloc(array.nbytes)
+        _check(_lib().ipus_buffer_upload(self.handle, buf.ptr, array.ctypes.data, array.nbytes))
+        return buf
+
+    def write(self, buf: DeviceBuffer, array: np.ndarray) -> None:
+        array = np.ascontiguousarray(array)
+        if array.nbytes > buf.nbytes:
+            raise ValueError("array larger than buffer")
+        _check(_lib().ipus_buffer_upload(self.handle, buf.ptr, array.ctypes.data, array.nbytes))
+
+    def download_into(self, buf: DeviceBuffer, out: np.ndarray) -> None:
+        if not out.flags.c_contiguous or out.nbytes > buf.nbytes:
+            raise ValueError("output must be contiguous and fit the buffer")
+        _check(_lib().ipus_buffer_download(self.handle, out.ctypes.data, buf.ptr, out.nbytes))
+
+    def memset(self, buf: DeviceBuffer, value: int = 0) -> None:
+        _check(_lib().ipus_buffer_memset(self.handle, buf.ptr, int(value), buf.nbytes))
+
+    def sync(self) -> None:
+        _check(_lib().ipus_stream_sync(self.handle))
+
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        _check(_lib().ipus_context_stream(self.handle, ctypes.byref(s)))
+        return s.value or 0
+
+    def launch(self, symbol: str, out, inputs: Sequence, scalars: Sequence[int]) -> None:
+        """One ComputeStep: symbol, output pointer, input pointers, u32 scalars."""
+        ptrs = [x.ptr if isinstance(x, DeviceBuffer) else int(x) for x in inputs]
+        in_arr = (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
+        sc, n = _u32_array(scalars)
+        outp = out.ptr if isinstance(out, DeviceBuffer) else int(out)
+        _check(_lib().ipus_launch(self.handle, symbol.encode(), outp, in_arr, len(ptrs), sc, n))
+
+    def timer(self) -> "Timer":
+        return Timer(self)
+
+
+class Timer:
+    """HIP events recorded on the context stream."""
+
+    def __init__(self, context: Context):
+        self.context = context
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(_lib().ipus_event_create(context.handle, ctypes.byref(a)))
+        _check(_lib().ipus_event_create(context.handle, ctypes.byref(b)))
+        self.start_event, self.end_event = a.value, b.value
+
+    def start(self) -> None:
+        _check(_lib().ipus_event_record(self.context.handle, self.start_event))
+
+    def stop(self) -> float:
+        """Records the end event and returns the elapsed milliseconds."""
+        _check(_lib().ipus_event_record(self.context.handle, self.end_event))
+        ms = ctypes.c_float(0)
+        _check(_lib().ipus_event_elapsed_ms(self.start_event, self.end_event, ctypes.byref(ms)))
+        return ms.value
+
+    def close(self) -> None:
+        _lib().ipus_event_destroy(self.start_event)
+        _lib().ipus_event_destroy(self.end_event)
+
+
+# ---------------------------------------------------------------------------
+# ComputeGraph (graph.rs) and build_package (package.rs)
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class RepeatArguments:
+    """graph.rs:196-201."""
+    carried: list
+    invariants: list
+    iterated: list
+
+
+class RegionBuilder:
+    """Body builder handed to ``ComputeGraph.repeat`` (graph.rs:517-632)."""
+
+    def __init__(self, graph: "ComputeGraph"):
+        self._graph = graph
+
+    def __getattr__(self, name):
+        if name in ("gemm", "gemm_with_options", "gelu", "add", "split_heads", "flash_attention",
+                    "flash_attention_with_options", "transpose", "rearrange", "reduce_rows",
+                    "value_shape", "repeat"):
+            return getattr(self._graph, name)
+        raise AttributeError(name)
+
+
+class ComputeGraph:
+    """Structured-SSA graph (crates/ipu-codegen/src/graph.rs:203-515)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _check(_lib().ipus_graph_create(ctypes.byref(h)))
+        self.handle = h.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                _lib().ipus_graph_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+    def _value(self, fn, *args) -> int:
+        out = ctypes.c_uint32(0)
+        _check(fn(self.handle, *args, ctypes.byref(out)))
+        return out.value
+
+    def host_input(self, name: str, shape: Sequence[int]) -> int:
+        dims, n = _u32_array(shape)
+        return self._value(_lib().ipus_graph_host_input, name.encode(), dims, n)
+
+    def parameter(self, name: str, shape: Sequence[int]) -> int:
+        dims, n = _u32_array(shape)
+        return self._value(_lib().ipus_graph_parameter, name.encode(), dims, n)
+
+    def value_sequence(self, name: str, values: Sequence[int]) -> int:
+        vs, n = _u32_array(values)
+        return self._value(_lib().ipus_graph_value_sequence, name.encode(), vs, n)
+
+    def gemm(self, left: int, right: int) -> int:
+        return self.gemm_with_options(left, right)
+
+    def gemm_with_options(self, left: int, right: int, transpose_left: bool = False,
+                          transpose_right: bool = False) -> int:
+        return self._value(_lib().ipus_graph_gemm, left, right, int(transpose_left),
+                           int(transpose_right))
+
+    def gelu(self, value: int) -> int:
+        return self._value(_lib().ipus_graph_gelu, value)
+
+    def add(self, left: int, right: int) -> int:
+        return self._value(_lib().ipus_graph_add, left, right)
+
+    def split_heads(self, value: int, heads: int) -> int:
+        return self._value(_lib().ipus_graph_split_heads, value, int(heads))
+
+    def flash_attention(self, query: int, key: int, value: int) -> int:
+        return self.flash_attention_with_options(query, key, value)
+
+    def flash_attention_with_options(self, query: int, key: int, value: int,
+                                     causal: bool = False, scale: float | None = None) -> int:
+        return self._value(_lib().ipus_graph_flash_attention, query, key, value, int(causal),
+                           int(scale is not None), 0 if scale is None else _f32_bits(scale))
+
+    def transpose(self, value: int) -> int:
+        return self._value(_lib().ipus_graph_transpose, value)
+
+    def rearrange(self, value: int, order: int, row_block: int = 0,
+                  column_block: int = 0) -> int:
+        return self._value(_lib().ipus_graph_rearrange, value, int(order), int(row_block),
+                           int(column_block))
+
+    def reduce_rows(self, value: int) -> int:
+        return self._value(_lib().ipus_graph_reduce_rows, value)
+
+    def repeat(self, count: int, carried: Sequence[int], invariants: Sequence[int],
+               iterated: Sequence[int], build: Callable) -> list:
+        """graph.rs:382-472: ``build(body, arguments) -> yields``."""
+        c, nc = _u32_array(carried)
+        i, ni = _u32_array(invariants)
+        s, ns = _u32_array(iterated)
+        args = (ctypes.c_uint32 * max(1, nc + ni + ns))()
+        _check(_lib().ipus_graph_repeat_begin(self.handle, int(count), c, nc, i, ni, s, ns, args))
+        a = list(args)[: nc + ni + ns]
+        arguments = RepeatArguments(a[:nc], a[nc:nc + ni], a[nc + ni:])
+        try:
+            yields = list(build(RegionBuilder(self), arguments))
+        except Exception:
+            # Drop the open body so the graph stays usable, then re-raise.
+            _lib().ipus_graph_repeat_abort(self.handle)
+            raise
+        y, ny = _u32_array(yields)
+        results = (ctypes.c_uint32 * max(1, ny))()
+        _check(_lib().ipus_graph_repeat_end(self.handle, y, ny, results))
+        return list(results)[:ny]
+
+    def set_outputs(self, values: Sequence[int]) -> None:
+        vs, n = _u32_array(values)
+        _check(_lib().ipus_graph_set_outputs(self.handle, vs, n))
+
+    def value_shape(self, value: int) -> tuple | None:
+        dims = (ctypes.c_uint32 * MAX_RANK)()
+        rank = ctypes.c_int(0)
+        status = _lib().ipus_graph_value_shape(self.handle, value, dims, MAX_RANK,
+                                               ctypes.byref(rank))
+        if status != 0:
+            return None
+        return tuple(dims[i] for i in range(rank.value))
+
+    def operation_count(self) -> int:
+        n = ctypes.c_int(0)
+        _check(_lib().ipus_graph_operation_count(self.handle, ctypes.byref(n)))
+        return n.value
+
+
+@dataclass
+class PackageConfig:
+    """GPU stand-in for PackageConfig (package.rs:89-94): compute precision
+    of GEMM / Add and the attention output precision."""
+    compute_precision: str = "f16"
+    attention_output_f16: bool = False
+
+
+@dataclass(frozen=True)
+class CompiledTensor:
+    """Binding metadata (CompiledTensor, package.rs:131-145)."""
+    name: str
+    value: int
+    shape: tuple
+    precision: int
+    order: int
+    row_block: int
+    column_block: int
+    nbytes: int
+
+    @property
+    def dtype(self):
+        return np.float32 if self.precision == PRECISION_F32 else np.uint16
+
+
+def _tensor(info: _TensorInfo) -> CompiledTensor:
+    return CompiledTensor(info.name.decode(), info.value,
+                          tuple(info.dims[i] for i in range(info.rank)), info.precision,
+                          info.order, info.row_block, info.column_block, info.bytes)
+
+
+class CompiledPackage:
+    def __init__(self, handle: int):
+        self.handle = handle
+        lib = _lib()
+        n = ctypes.c_int(0)
+        _check(lib.ipus_package_input_count(handle, ctypes.byref(n)))
+        self.inputs = []
+        for i in range(n.value):
+            info = _TensorInfo()
+            _check(lib.ipus_package_input_info(handle, i, ctypes.byref(info)))
+            self.inputs.append(_tensor(info))
+        _check(lib.ipus_package_output_count(handle, ctypes.byref(n)))
+        self.outputs = []
+        for i in range(n.value):
+            info = _TensorInfo()
+            _check(lib.ipus_package_output_info(handle, i, ctypes.byref(info)))
+            self.outputs.append(_tensor(info))
+        _check(lib.ipus_package_step_count(handle, ctypes.byref(n)))
+        self.steps = []
+        for i in range(n.value):
+            sym = ctypes.c_char_p()
+            ni, ns = ctypes.c_int(0), ctypes.c_int(0)
+            sc = _U32P()
+            _check(lib.ipus_package_step(handle, i, ctypes.byref(sym), ctypes.byref(ni),
+                                         ctypes.byref(ns), ctypes.byref(sc)))
+            self.steps.append((sym.value.decode(), ni.value,
+                               tuple(sc[k] for k in range(ns.value))))
+        a = ctypes.c_uint64(0)
+        _check(lib.ipus_package_arena_bytes(handle, ctypes.byref(a)))
+        self.arena_bytes = a.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                _lib().ipus_package_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+    def precision(self, value: int) -> int:
+        p = ctypes.c_int(0)
+        _check(_lib().ipus_package_value_precision(self.handle, value, ctypes.byref(p)))
+        return p.value
+
+    def session(self, context: Context) -> "Session":
+        return Session(context, self)
+
+
+def build_package(graph: ComputeGraph, config: PackageConfig | None = None) -> CompiledPackage:
+    """package.rs:532-538 for the GPU plan."""
+    config = config or PackageConfig()
+    c = _PackageConfig(PRECISION_F32 if config.compute_precision == "f32" else PRECISION_F16,
+                       int(config.attention_output_f16))
+    h = ctypes.c_void_p()
+    _check(_lib().ipus_build_package(graph.handle, ctypes.byref(c), ctypes.byref(h)))
+    return CompiledPackage(h.value)
+
+
+class Session:
+    """Device buffers for one package (HostSession role)."""
+
+    def __init__(self, context: Context, package: CompiledPackage):
+        self.context = context
+        self.package = package
+        h = ctypes.c_void_p()
+        _check(_lib().ipus_session_create(context.handle, package.handle, ctypes.byref(h)))
+        self.handle = h.value
+        self._meta = {t.name: t for t in package.inputs + package.outputs}
+
+    def close(self) -> None:
+        if self.handle:
+            _lib().ipus_session_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def write(self, name: str, array: np.ndarray) -> None:
+        array = np.ascontiguousarray(array)
+        _check(_lib().ipus_session_write(self.handle, name.encode(), array.ctypes.data,
+                                         array.nbytes))
+
+    def read(self, name: str) -> np.ndarray:
+        meta = self._meta[name]
+        out = np.empty(meta.shape, dtype=meta.dtype)
+        _check(_lib().ipus_session_read(self.handle, name.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def pointer(self, name: str) -> int:
+        p = ctypes.c_void_p()
+        _check(_lib().ipus_session_tensor_pointer(self.handle, name.encode(), ctypes.byref(p)))
+        return p.value
+
+    def run(self) -> None:
+        _check(_lib().ipus_session_run(self.handle))
+
+    def run_sync(self) -> None:
+        self.run()
+        self.context.sync()

@@ -1,0 +1,243 @@
+// fp32 GEMM on gfx950 MFMA (v_mfma_f32_32x32x2_f32), fp32 accumulation and
+// output: replaces gemm_f32_64_amp (device/gemm_f32_64_amp.S:125-385), whose
+// init mode clears the output and accumulates in fp32 (gemm_f32_64_amp.S:40-56).
+//
+// Fast kernel (M % 128 == 0, N % 128 == 0, K % 32 == 0):
+//   * block tile 128 x 128 x 32, 4 waves in a 2 x 2 grid, each wave 64 x 64
+//     as 2 x 2 MFMA tiles;
+//   * operands staged in LDS k-major ([k][m], [k][n]) so a fragment is 32
+//     consecutive floats of one k row; the 16-byte chunk index is XOR-swizzled
+//     by (k >> 2) & 7 so the transposing tile stores are conflict-free;
+//   * a K-contiguous operand (row-major A, transposed B) is transposed in
+//     registers on 4 x 4 blocks before its LDS store;
+//   * two LDS stages, loads for the next K step in flight during the MFMAs;
+//   * the MFMA computes C^T tiles so each lane holds 4 consecutive columns
+//     of C (one 16-byte store).
+#include "../../include/ipus.h"
+#include "device_common.h"
+#include "kernels.h"
+
+namespace ipus {
+namespace {
+
+constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kThreads = 256;
+constexpr int kTileBytes = kBK * kBM * 4;  // 16 KiB per operand tile
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
+
+// Byte offset of element (k, x) in a [32][128] fp32 tile.
+__device__ __forceinline__ uint32_t swz32(uint32_t k, uint32_t x) {
+  return k * 512u + ((((x >> 2) ^ ((k >> 2) & 7u)) << 4) | ((x & 3u) << 2));
+}
+
+// Loads a 128 (x) by 32 (k) operand tile.
+// XContig: element (x, k) at base[(k0 + k) * ld + x0 + x]  (stored [K][X])
+// else:    element (x, k) at base[(x0 + x) * ld + k0 + k]  (stored [X][K])
+template <bool XContig>
+__device__ __forceinline__ void load_tile32(const float* __restrict__ base, uint64_t ld,
+                                            uint32_t x0, uint32_t k0, u32x4 v[4]) {
+  const uint32_t t = threadIdx.x;
+  if constexpr (XContig) {
+    const float* p = base + (uint64_t)(k0 + t / 32) * ld + x0 + (t % 32) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load16(p + (uint64_t)(8 * i) * ld);
+  } else {
+    const float* p = base + (uint64_t)(x0 + (t / 8) * 4) * ld + k0 + (t % 8) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = load16(p + (uint64_t)j * ld);
+  }
+}
+
+template <bool XContig>
+__device__ __forceinline__ void store_tile32(uint8_t* lds, const u32x4 v[4]) {
+  const uint32_t t = threadIdx.x;
+  if constexpr (XContig) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(lds + swz32(t / 32 + 8 * i, (t % 32) * 4)) = v[i];
+  } else {
+    // v[j] = x row (t/8)*4 + j, k = (t%8)*4 .. +3 ; w[i] = k row (t%8)*4 + i.
+    u32x4 w[4];
+    transpose4x4_u32(v, w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(lds + swz32((t % 8) * 4 + i, (t / 8) * 4)) = w[i];
+  }
+}
+
+__device__ __forceinline__ float read32(const uint8_t* lds, uint32_t k, uint32_t x) {
+  return *reinterpret_cast<const float*>(lds + swz32(k, x));
+}
+
+template <bool TransposeLeft, bool TransposeRight>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_128_kernel(
+    float* __restrict__ out, const float* __restrict__ left, const float* __restrict__ right,
+    uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kTileBytes];
+
+  const uint32_t nbm = M / kBM, nbn = N / kBN;
+  const uint32_t tiles = nbm * nbn;
+  uint32_t pid = blockIdx.x;
+  if (tiles % 8 == 0) pid = (pid % 8) * (tiles / 8) + pid / 8;
+  constexpr uint32_t kGroup = 8;
+  const uint32_t group = pid / (kGroup * nbn);
+  const uint32_t first_m = group * kGroup;
+  const uint32_t group_rows = (nbm - first_m) < kGroup ? (nbm - first_m) : kGroup;
+  const uint32_t in_group = pid % (kGroup * nbn);
+  const uint32_t bm = first_m + in_group % group_rows;
+  const uint32_t bn = in_group / group_rows;
+
+  const uint64_t batch = blockIdx.y;
+  const float* A = left + batch * left_batch_stride;
+  const float* B = right + batch * right_batch_stride;
+  float* C = out + batch * (uint64_t)M * N;
+  const uint64_t lda = TransposeLeft ? M : K;
+  const uint64_t ldb = TransposeRight ? K : N;
+  constexpr bool kAX = TransposeLeft;    // A stored [K][M]: m contiguous
+  constexpr bool kBX = !TransposeRight;  // B stored [K][N]: n contiguous
+
+  const uint32_t m0 = bm * kBM, n0 = bn * kBN;
+  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const uint32_t wm = (wave / 2) * 64, wn = (wave % 2) * 64;
+
+  float16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  u32x4 ra[4], rb[4];
+  load_tile32<kAX>(A, lda, m0, 0, ra);
+  load_tile32<kBX>(B, ldb, n0, 0, rb);
+  store_tile32<kAX>((smem + 0 + (0) * 2 * kTileBytes), ra);
+  store_tile32<kBX>((smem + kTileBytes + (0) * 2 * kTileBytes), rb);
+  __syncthreads();
+
+  const uint32_t ksteps = K / kBK;
+  for (uint32_t kt = 0; kt < ksteps; ++kt) {
+    const uint32_t cur = kt & 1;
+    const bool more = kt + 1 < ksteps;
+    if (more) {
+      load_tile32<kAX>(A, lda, m0, (kt + 1) * kBK, ra);
+      load_tile32<kBX>(B, ldb, n0, (kt + 1) * kBK, rb);
+    }
+    const uint8_t* la = (smem + 0 + (cur) * 2 * kTileBytes);
+    const uint8_t* lb = (smem + kTileBytes + (cur) * 2 * kTileBytes);
+#pragma unroll
+    for (uint32_t p = 0; p < kBK / 2; ++p) {
+      const uint32_t k = 2 * p + lane / 32;
+      float fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = read32(la, k, wm + 32 * i + lane % 32);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = read32(lb, k, wn + 32 * j + lane % 32);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      store_tile32<kAX>((smem + 0 + (cur ^ 1) * 2 * kTileBytes), ra);
+      store_tile32<kBX>((smem + kTileBytes + (cur ^ 1) * 2 * kTileBytes), rb);
+    }
+    __syncthreads();
+  }
+
+  const uint32_t row = m0 + wm + lane % 32;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float* crow = C + (uint64_t)(row + 32 * i) * N + n0 + wn + 4 * (lane / 32);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+        *reinterpret_cast<float4_t*>(crow + 32 * j + 8 * g) = v;
+      }
+  }
+}
+
+// General fp32 GEMM: 64 x 64 tile, 4 waves of one 32 x 32 MFMA tile, K step 8.
+__global__ __launch_bounds__(256) void gemm_f32_general_kernel(
+    float* __restrict__ out, const float* __restrict__ left, const float* __restrict__ right,
+    uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr, uint64_t left_batch_stride,
+    uint64_t right_batch_stride, uint32_t tiles_n) {
+  __shared__ float As[8][64];
+  __shared__ float Bs[8][64];
+  const uint64_t batch = blockIdx.y;
+  const float* A = left + batch * left_batch_stride;
+  const float* B = right + batch * right_batch_stride;
+  float* C = out + batch * (uint64_t)M * N;
+  const uint32_t m0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
+  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const uint32_t wm = (wave / 2) * 32, wn = (wave % 2) * 32;
+  const uint64_t lda = tl ? M : K, ldb = tr ? K : N;
+  float16_t acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (uint32_t k0 = 0; k0 < K; k0 += 8) {
+    for (uint32_t idx = threadIdx.x; idx < 64 * 8; idx += 256) {
+      const uint32_t k = idx / 64, x = idx % 64;
+      const uint32_t m = m0 + x, n = n0 + x, kk = k0 + k;
+      float a = 0.0f, b = 0.0f;
+      if (m < M && kk < K) a = tl ? A[(uint64_t)kk * lda + m] : A[(uint64_t)m * lda + kk];
+      if (n < N && kk < K) b = tr ? B[(uint64_t)n * ldb + kk] : B[(uint64_t)kk * ldb + n];
+      As[k][x] = a;
+      Bs[k][x] = b;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t k = 2 * p + lane / 32;
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Bs[k][wn + lane % 32], As[k][wm + lane % 32], acc,
+                                                 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  const uint32_t m = m0 + wm + lane % 32;
+  if (m >= M) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t n = n0 + wn + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+    if (n < N) C[(uint64_t)m * N + n] = acc[r];
+  }
+}
+
+template <bool TL, bool TR>
+int launch_fast(hipStream_t stream, const GemmArgs& a) {
+  const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
+  hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR>), dim3(tiles, a.batches), dim3(kThreads), 0,
+                     stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
+                     a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  return hip_status(hipGetLastError());
+}
+
+}  // namespace
+
+int launch_gemm_f32(hipStream_t stream, const GemmArgs& a) {
+  if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
+  if (a.batches > 65535) return IPUS_ERROR_INVALID_ARGUMENT;
+  const bool aligned = ((uintptr_t)a.left % 16 == 0) && ((uintptr_t)a.right % 16 == 0) &&
+                       ((uintptr_t)a.out % 16 == 0) && a.left_batch_stride % 4 == 0 &&
+                       a.right_batch_stride % 4 == 0;
+  if (aligned && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner % kBK == 0 && a.inner > 0) {
+    if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
+    if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
+    if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);
+    return launch_fast<true, true>(stream, a);
+  }
+  const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
+  hipLaunchKernelGGL(gemm_f32_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
+                     stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
+                     a.columns, a.inner, a.transpose_left, a.transpose_right, a.left_batch_stride,
+                     a.right_batch_stride, tiles_n);
+  return hip_status(hipGetLastError());
+}
+
+}  // namespace ipus

@@ -1,0 +1,686 @@
+// Bandwidth-bound kernels for gfx950: transpose, rearranges into the
+// reference's storage orders, unpack, row reduction, the reference's
+// partial-sum reduction, GELU, casts, add and split_heads.
+//
+// Design: every hot kernel moves 16-byte vectors per lane and keeps each
+// wave's global accesses in whole 128-byte lines.  Transposes of 16-bit data
+// are done in registers on 8x8 blocks (no LDS, no bank conflicts): a lane
+// reads 8 rows x 16 bytes and writes 8 rows x 16 bytes.
+#include "../../include/ipus.h"
+#include "device_common.h"
+#include "kernels.h"
+#include "layout_maps.h"
+
+namespace ipus {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Transpose: [matrices][rows][columns] -> [matrices][columns][rows].
+// A wave owns a 64x64 tile; lane (rc = lane % 8, cc = lane / 8) owns the 8x8
+// block at rows 8*rc, columns 8*cc.  For each of the 8 loads the wave reads 8
+// rows x 128 contiguous bytes; for each store it writes 8 rows x 128 bytes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void transpose_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t columns,
+    uint32_t tiles_c) {
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  // Block covers 128 x 128 (2 x 2 wave tiles).
+  const uint32_t block_r = (blockIdx.x / tiles_c) * 128 + (wave / 2) * 64;
+  const uint32_t block_c = (blockIdx.x % tiles_c) * 128 + (wave % 2) * 64;
+  const uint64_t matrix = blockIdx.y;
+  const uint32_t r0 = block_r + (lane % 8) * 8;
+  const uint32_t c0 = block_c + (lane / 8) * 8;
+  if (r0 >= rows || c0 >= columns) return;
+  const uint16_t* s = src + matrix * rows * (uint64_t)columns;
+  uint16_t* d = dst + matrix * rows * (uint64_t)columns;
+  u32x4 in[8], out[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) in[j] = load16(s + (uint64_t)(r0 + j) * columns + c0);
+  transpose8x8_u16(in, out);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) store16(d + (uint64_t)(c0 + i) * rows + r0, out[i]);
+}
+
+__global__ __launch_bounds__(kThreads) void transpose_f16_scalar_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t columns,
+    uint64_t total) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint64_t matrix = idx / me;
+  const uint64_t within = idx % me;  // index in the destination [columns][rows]
+  const uint32_t c = (uint32_t)(within / rows);
+  const uint32_t r = (uint32_t)(within % rows);
+  dst[idx] = src[matrix * me + (uint64_t)r * columns + c];
+}
+
+// ---------------------------------------------------------------------------
+// Row-major -> BlockMajor{row_block, column_block} without padding.  Inside a
+// micro-panel the 16 rows of one column are contiguous, so an 8x8 register
+// transpose turns 8 source rows into 8 destination runs of 8 rows.  A wave
+// covers 16 rows x 256 columns: lane % 2 picks the row half, lane / 2 the
+// 8-column chunk.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void block_major_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t columns,
+    uint32_t row_block, uint32_t column_block, uint32_t tiles_c) {
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t r0 = (blockIdx.x / tiles_c) * 64 + wave * 16 + (lane % 2) * 8;
+  const uint32_t c0 = (blockIdx.x % tiles_c) * 256 + (lane / 2) * 8;
+  if (r0 >= rows || c0 >= columns) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint16_t* s = src + blockIdx.y * me;
+  uint16_t* d = dst + blockIdx.y * me;
+  u32x4 in[8], out[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) in[j] = load16(s + (uint64_t)(r0 + j) * columns + c0);
+  transpose8x8_u16(in, out);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    store16(d + block_major_index(row_block, column_block, columns, r0, c0 + i), out[i]);
+}
+
+// ---------------------------------------------------------------------------
+// General rearrange / unpack: one thread per destination element, gathering
+// from the source through the inverse (or forward) storage map, zero-filling
+// padding.  Used for padded or unaligned shapes and the AMP orders.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void rearrange_f16_general_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t target_order,
+    uint32_t row_block, uint32_t column_block, uint32_t matrices, uint32_t logical_rows,
+    uint32_t physical_rows, uint32_t logical_columns, uint32_t physical_columns, uint64_t total) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const uint64_t me = (uint64_t)physical_rows * physical_columns;
+  uint32_t matrix, row, column;
+  if (target_order == kOrderAmpLeft) {
+    // Outer matrices fold into the row axis (storage.rs:250-266).
+    uint32_t flat_row;
+    amp_left_coordinates(matrices * physical_rows, idx, &flat_row, &column);
+    matrix = flat_row / physical_rows;
+    row = flat_row % physical_rows;
+  } else {
+    matrix = (uint32_t)(idx / me);
+    const uint64_t within = idx % me;
+    if (target_order == kOrderAmpTransposedRight)
+      amp_transposed_right_coordinates(physical_rows, physical_columns, within, &row, &column);
+    else
+      block_major_coordinates(row_block, column_block, physical_columns, within, &row, &column);
+  }
+  uint16_t v = 0;
+  if (row < logical_rows && column < logical_columns)
+    v = src[((uint64_t)matrix * logical_rows + row) * logical_columns + column];
+  dst[idx] = v;
+}
+
+__global__ __launch_bounds__(kThreads) void unpack_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t source_order,
+    uint32_t logical_rows, uint32_t physical_rows, uint32_t logical_columns,
+    uint32_t physical_columns, uint64_t total) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const uint64_t me = (uint64_t)physical_rows * physical_columns;
+  const uint64_t matrix = idx / me;
+  const uint64_t within = idx % me;
+  const uint32_t row = (uint32_t)(within / physical_columns);
+  const uint32_t column = (uint32_t)(within % physical_columns);
+  uint16_t v = 0;
+  if (row < logical_rows && column < logical_columns) {
+    const uint64_t physical =
+        source_order == kUnpackAmpOutput
+            ? amp_output_index(physical_rows, row, column)
+            : amp_transposed_left_index(physical_rows, physical_columns, row, column);
+    v = src[matrix * me + physical];
+  }
+  dst[idx] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Row sums of a row-major [rows, columns] fp16 matrix, fp32 accumulation.
+// One block per row; 16-byte loads; wave shuffles then LDS across waves.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sum8_f16(u32x4 v) {
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = v[w];
+    s += (float)__builtin_bit_cast(half_t, (uint16_t)(x & 0xffffu));
+    s += (float)__builtin_bit_cast(half_t, (uint16_t)(x >> 16));
+  }
+  return s;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* shared) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) shared[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) total += shared[w];
+  return total;
+}
+
+__global__ __launch_bounds__(kThreads) void reduce_rows_f16_kernel(
+    float* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t columns) {
+  __shared__ float partial[kThreads / kWave];
+  const uint16_t* row = src + (uint64_t)blockIdx.x * columns;
+  float acc = 0.0f;
+  const uint32_t vectors = columns / 8;
+  for (uint32_t v = threadIdx.x; v < vectors; v += kThreads) acc += sum8_f16(load16(row + v * 8));
+  for (uint32_t c = vectors * 8 + threadIdx.x; c < columns; c += kThreads)
+    acc += (float)__builtin_bit_cast(half_t, row[c]);
+  const float total = block_sum(acc, partial);
+  if (threadIdx.x == 0) dst[blockIdx.x] = total;
+}
+
+// Unaligned rows (columns not a multiple of 8): scalar loads.
+__global__ __launch_bounds__(kThreads) void reduce_rows_f16_scalar_kernel(
+    float* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t columns) {
+  __shared__ float partial[kThreads / kWave];
+  const uint16_t* row = src + (uint64_t)blockIdx.x * columns;
+  float acc = 0.0f;
+  for (uint32_t c = threadIdx.x; c < columns; c += kThreads)
+    acc += (float)__builtin_bit_cast(half_t, row[c]);
+  const float total = block_sum(acc, partial);
+  if (threadIdx.x == 0) dst[blockIdx.x] = total;
+}
+
+// Row sums of a logical [rows, columns] matrix stored BlockMajor{rb, cb}.
+// The 16 rows of one row group live in columns/cb panels of 16*cb elements
+// (column-major inside a panel), panel stride rb/16 panels.  Block (group,
+// split) walks one column range of a row group; lane parity selects the row
+// half, so each lane accumulates 8 rows.  Partial sums go to
+// workspace[split][rows]; a second kernel adds the splits in order.
+constexpr uint32_t kReduceSplits = 4;
+
+__global__ __launch_bounds__(kThreads) void reduce_rows_block_major_kernel(
+    float* __restrict__ workspace, const uint16_t* __restrict__ src, uint32_t rows,
+    uint32_t columns, uint32_t row_block, uint32_t column_block) {
+  __shared__ float partial[kThreads / kWave][16];
+  const uint32_t group = blockIdx.x;  // 16-row group
+  const uint32_t split = blockIdx.y;
+  const uint32_t row0 = group * 16;
+  const uint32_t row_groups = row_block / 16;
+  const uint32_t column_blocks = columns / column_block;
+  // First panel of this row group (column block 0).
+  const uint64_t first_panel =
+      (uint64_t)(row0 / row_block) * column_blocks * row_groups + (row0 % row_block) / 16;
+  const uint32_t vectors_per_panel = column_block * 2;  // 16 rows x cb columns / 8
+  const uint32_t total_vectors = column_blocks * vectors_per_panel;
+  // Split points are rounded down to even vectors (total_vectors is even), so
+  // v % 2 == threadIdx.x % 2 for every v this thread visits: each lane always
+  // sees the same row half.
+  const uint32_t begin = (uint32_t)((uint64_t)total_vectors * split / kReduceSplits) & ~1u;
+  const uint32_t end = split + 1 == kReduceSplits
+                           ? total_vectors
+                           : (uint32_t)((uint64_t)total_vectors * (split + 1) / kReduceSplits) & ~1u;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (uint32_t v = begin + threadIdx.x; v < end; v += kThreads) {
+    const uint32_t panel_index = v / vectors_per_panel;
+    const uint32_t within = v % vectors_per_panel;
+    const uint64_t element =
+        (first_panel + (uint64_t)panel_index * row_groups) * 16 * column_block + within * 8;
+    const u32x4 x = load16(src + element);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      acc[2 * w] += (float)__builtin_bit_cast(half_t, (uint16_t)(x[w] & 0xffffu));
+      acc[2 * w + 1] += (float)__builtin_bit_cast(half_t, (uint16_t)(x[w] >> 16));
+    }
+  }
+  // Reduce over lanes of equal parity.
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float s = acc[e];
+#pragma unroll
+    for (int offset = 32; offset >= 2; offset >>= 1) s += __shfl_xor(s, offset, kWave);
+    acc[e] = s;
+  }
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (lane < 2) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) partial[wave][lane * 8 + e] = acc[e];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float s = 0.0f;
+    for (uint32_t w = 0; w < kThreads / kWave; ++w) s += partial[w][threadIdx.x];
+    workspace[(uint64_t)split * rows + row0 + threadIdx.x] = s;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void reduce_splits_kernel(float* __restrict__ dst,
+                                                                 const float* __restrict__ workspace,
+                                                                 uint32_t rows) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float s = 0.0f;
+  for (uint32_t k = 0; k < kReduceSplits; ++k) s += workspace[(uint64_t)k * rows + r];
+  dst[r] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Reference ReductionSum: out = initial + remote[0] + ... + remote[P-1],
+// each addition rounded to fp16 in order (device/reduce_add_f16.S:54-70).
+// ---------------------------------------------------------------------------
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__global__ __launch_bounds__(kThreads) void reduce_sum_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ initial,
+    const uint16_t* __restrict__ remote, uint32_t partials, uint32_t count) {
+  const uint32_t vectors = count / 8;
+  for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < vectors;
+       v += gridDim.x * blockDim.x) {
+    half8_t acc = __builtin_bit_cast(half8_t, load16(initial + (uint64_t)v * 8));
+    for (uint32_t p = 0; p < partials; ++p)
+      acc = acc + __builtin_bit_cast(half8_t, load16(remote + (uint64_t)p * count + (uint64_t)v * 8));
+    store16(dst + (uint64_t)v * 8, __builtin_bit_cast(u32x4, acc));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tanh-approximate GELU, fp32 internally:
+//   0.5 x (1 + tanh(u)) = x * sigmoid(2u) = x / (1 + exp(-2u)),
+//   u = 0.7978846 (x + 0.044715 x^3)   (crates/ipu-tests/src/main.rs:1985-1987)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float u = 0.7978846f * (x + 0.044715f * x * x * x);
+  return x / (1.0f + expf(-2.0f * u));
+}
+
+__device__ __forceinline__ uint32_t gelu_pair(uint32_t bits) {
+  const half2_t h = __builtin_bit_cast(half2_t, bits);
+  half2_t r;
+  r[0] = (half_t)gelu_tanh((float)h[0]);
+  r[1] = (half_t)gelu_tanh((float)h[1]);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__global__ __launch_bounds__(kThreads) void gelu_f16_kernel(uint16_t* __restrict__ dst,
+                                                            const uint16_t* __restrict__ src,
+                                                            uint64_t count) {
+  const uint64_t vectors = count / 8;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v < vectors; v += stride) {
+    u32x4 x = load16(src + v * 8);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x[w] = gelu_pair(x[w]);
+    store16(dst + v * 8, x);
+  }
+  // Tail elements.
+  const uint64_t tail = vectors * 8 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tail < count && tail < vectors * 8 + 8) {
+    const half_t h = __builtin_bit_cast(half_t, src[tail]);
+    dst[tail] = __builtin_bit_cast(uint16_t, (half_t)gelu_tanh((float)h));
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gelu_f16_scalar_kernel(uint16_t* __restrict__ dst,
+                                                                   const uint16_t* __restrict__ src,
+                                                                   uint64_t count) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const half_t h = __builtin_bit_cast(half_t, src[i]);
+    dst[i] = __builtin_bit_cast(uint16_t, (half_t)gelu_tanh((float)h));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fill, casts, add, split_heads.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(uint8_t* __restrict__ dst,
+                                                             uint64_t bytes) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t vectors = bytes / 16;
+  for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v < vectors; v += stride)
+    store16(dst + v * 16, u32x4{0, 0, 0, 0});
+  const uint64_t tail = vectors * 16 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tail < bytes && tail < vectors * 16 + 16) dst[tail] = 0;
+}
+
+__global__ __launch_bounds__(kThreads) void cast_f32_f16_kernel(uint16_t* __restrict__ dst,
+                                                                const float* __restrict__ src,
+                                                                uint64_t count) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride)
+    dst[i] = __builtin_bit_cast(uint16_t, (half_t)src[i]);
+}
+
+__global__ __launch_bounds__(kThreads) void cast_f16_f32_kernel(float* __restrict__ dst,
+                                                                const uint16_t* __restrict__ src,
+                                                                uint64_t count) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride)
+    dst[i] = (float)__builtin_bit_cast(half_t, src[i]);
+}
+
+struct AddShape {
+  int rank;
+  uint32_t shape[6];
+  uint64_t ls[6];
+  uint64_t rs[6];
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void add_kernel(T* __restrict__ dst,
+                                                       const T* __restrict__ left,
+                                                       const T* __restrict__ right, AddShape s,
+                                                       uint64_t total) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    uint64_t rem = i, lo = 0, ro = 0;
+    for (int axis = s.rank - 1; axis >= 0; --axis) {
+      const uint64_t c = rem % s.shape[axis];
+      rem /= s.shape[axis];
+      lo += c * s.ls[axis];
+      ro += c * s.rs[axis];
+    }
+    if constexpr (sizeof(T) == 2) {
+      const float v = (float)__builtin_bit_cast(half_t, left[lo]) +
+                      (float)__builtin_bit_cast(half_t, right[ro]);
+      dst[i] = __builtin_bit_cast(uint16_t, (half_t)v);
+    } else {
+      dst[i] = left[lo] + right[ro];
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void split_heads_kernel(
+    T* __restrict__ dst, const T* __restrict__ src, uint32_t rows, uint32_t heads,
+    uint32_t channels, uint64_t total) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    // i indexes the destination [batch*heads, rows, channels].
+    const uint32_t c = (uint32_t)(i % channels);
+    uint64_t rem = i / channels;
+    const uint32_t r = (uint32_t)(rem % rows);
+    rem /= rows;
+    const uint32_t h = (uint32_t)(rem % heads);
+    const uint64_t b = rem / heads;
+    const uint64_t width = (uint64_t)heads * channels;
+    dst[i] = src[(b * rows + r) * width + (uint64_t)h * channels + c];
+  }
+}
+
+// Any stored order -> row-major [matrices][rows][columns], one thread per
+// destination element (forward storage maps, storage.rs:301-426).
+__global__ __launch_bounds__(kThreads) void to_row_major_f16_general_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t source_order,
+    uint32_t row_block, uint32_t column_block, uint32_t matrices, uint32_t rows,
+    uint32_t columns, uint64_t total) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint32_t matrix = (uint32_t)(idx / me);
+  const uint64_t within = idx % me;
+  const uint32_t row = (uint32_t)(within / columns), column = (uint32_t)(within % columns);
+  uint64_t physical;
+  if (source_order == kOrderAmpLeft)
+    physical = amp_left_index(matrices * rows, matrix * rows + row, column);
+  else if (source_order == kOrderAmpTransposedRight)
+    physical = matrix * me + amp_transposed_right_index(rows, columns, row, column);
+  else
+    physical = matrix * me + block_major_index(row_block, column_block, columns, row, column);
+  dst[idx] = src[physical];
+}
+
+// Block-major -> row-major, the inverse of block_major_f16_kernel: 8 runs of
+// 8 rows are read, transposed in registers and written as 8 row segments.
+__global__ __launch_bounds__(kThreads) void block_major_to_row_major_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t columns,
+    uint32_t row_block, uint32_t column_block, uint32_t tiles_c) {
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t r0 = (blockIdx.x / tiles_c) * 64 + wave * 16 + (lane % 2) * 8;
+  const uint32_t c0 = (blockIdx.x % tiles_c) * 256 + (lane / 2) * 8;
+  if (r0 >= rows || c0 >= columns) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint16_t* s = src + blockIdx.y * me;
+  uint16_t* d = dst + blockIdx.y * me;
+  u32x4 in[8], out[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    in[i] = load16(s + block_major_index(row_block, column_block, columns, r0, c0 + i));
+  transpose8x8_u16(in, out);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) store16(d + (uint64_t)(r0 + j) * columns + c0, out[j]);
+}
+
+inline uint32_t grid_for(uint64_t work_items, uint32_t cap = 256u * 32u) {
+  uint64_t g = (work_items + kThreads - 1) / kThreads;
+  if (g == 0) g = 1;
+  return (uint32_t)(g < cap ? g : cap);
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+int launch_transpose_f16(hipStream_t stream, void* dst, const void* src, uint32_t matrices,
+                         uint32_t rows, uint32_t columns) {
+  if (matrices == 0 || rows == 0 || columns == 0) return 0;
+  if (rows % 8 == 0 && columns % 8 == 0 && aligned16(dst) && aligned16(src) && matrices <= 65535) {
+    const uint32_t tiles_r = ceil_div(rows, 128), tiles_c = ceil_div(columns, 128);
+    hipLaunchKernelGGL(transpose_f16_kernel, dim3(tiles_r * tiles_c, matrices), dim3(kThreads), 0,
+                       stream, (uint16_t*)dst, (const uint16_t*)src, rows, columns, tiles_c);
+  } else {
+    const uint64_t total = (uint64_t)matrices * rows * columns;
+    hipLaunchKernelGGL(transpose_f16_scalar_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads),
+                       0, stream, (uint16_t*)dst, (const uint16_t*)src, rows, columns, total);
+  }
+  return hip_status(hipGetLastError());
+}
+
+int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_t target_order,
+                         uint32_t row_block, uint32_t column_block, uint32_t matrices,
+                         uint32_t logical_rows, uint32_t physical_rows, uint32_t logical_columns,
+                         uint32_t physical_columns) {
+  if (target_order > kOrderBlockMajor) return IPUS_ERROR_UNAVAILABLE;
+  if (logical_rows > physical_rows || logical_columns > physical_columns)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  // Storage constraints of each order (storage.rs:314-425).
+  if (target_order == kOrderAmpLeft && physical_columns % kMicro != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (target_order == kOrderAmpTransposedRight &&
+      (physical_rows % kMicro != 0 || physical_columns % kMicro != 0))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (target_order == kOrderBlockMajor &&
+      (row_block == 0 || column_block == 0 || row_block % kMicro != 0 ||
+       physical_rows % row_block != 0 || physical_columns % column_block != 0))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  const uint64_t total = (uint64_t)matrices * physical_rows * physical_columns;
+  if (total == 0) return 0;
+  const bool fast_block_major = target_order == kOrderBlockMajor &&
+                                logical_rows == physical_rows &&
+                                logical_columns == physical_columns && column_block % 8 == 0 &&
+                                aligned16(dst) && aligned16(src) && matrices <= 65535;
+  if (fast_block_major) {
+    const uint32_t tiles_r = ceil_div(physical_rows, 64), tiles_c = ceil_div(physical_columns, 256);
+    hipLaunchKernelGGL(block_major_f16_kernel, dim3(tiles_r * tiles_c, matrices), dim3(kThreads), 0,
+                       stream, (uint16_t*)dst, (const uint16_t*)src, physical_rows,
+                       physical_columns, row_block, column_block, tiles_c);
+  } else {
+    hipLaunchKernelGGL(rearrange_f16_general_kernel, dim3(ceil_div(total, kThreads)),
+                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
+                       target_order, row_block, column_block, matrices, logical_rows,
+                       physical_rows, logical_columns, physical_columns, total);
+  }
+  return hip_status(hipGetLastError());
+}
+
+int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
+                      uint32_t matrices, uint32_t logical_rows, uint32_t physical_rows,
+                      uint32_t logical_columns, uint32_t physical_columns) {
+  if (source_order > kUnpackAmpTransposedLeft) return IPUS_ERROR_UNAVAILABLE;
+  if (logical_rows > physical_rows || logical_columns > physical_columns)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  // device/unpack_amp_f16.cpp:24-27 static asserts.
+  if (source_order == kUnpackAmpOutput && physical_columns % kMicro != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (source_order == kUnpackAmpTransposedLeft && physical_rows % kMicro != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (physical_columns % 2 != 0) return IPUS_ERROR_INVALID_ARGUMENT;
+  const uint64_t total = (uint64_t)matrices * physical_rows * physical_columns;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(unpack_f16_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads), 0, stream,
+                     (uint16_t*)dst, (const uint16_t*)src, source_order, logical_rows,
+                     physical_rows, logical_columns, physical_columns, total);
+  return hip_status(hipGetLastError());
+}
+
+size_t reduce_rows_workspace_bytes(uint32_t source_order, uint32_t rows, uint32_t columns) {
+  (void)columns;
+  return source_order == kOrderBlockMajor ? sizeof(float) * kReduceSplits * (size_t)rows : 0;
+}
+
+int launch_reduce_rows_f16(hipStream_t stream, float* dst, const void* src, uint32_t source_order,
+                           uint32_t row_block, uint32_t column_block, uint32_t rows,
+                           uint32_t columns, float* workspace) {
+  if (rows == 0) return 0;
+  if (source_order == kOrderRowMajor) {
+    if (columns % 8 == 0 && aligned16(src))
+      hipLaunchKernelGGL(reduce_rows_f16_kernel, dim3(rows), dim3(kThreads), 0, stream, dst,
+                         (const uint16_t*)src, columns);
+    else
+      hipLaunchKernelGGL(reduce_rows_f16_scalar_kernel, dim3(rows), dim3(kThreads), 0, stream, dst,
+                         (const uint16_t*)src, columns);
+    return hip_status(hipGetLastError());
+  }
+  if (source_order != kOrderBlockMajor) return IPUS_ERROR_UNAVAILABLE;
+  if (row_block == 0 || column_block == 0 || row_block % kMicro != 0 || rows % row_block != 0 ||
+      columns % column_block != 0 || column_block % 2 != 0 || !aligned16(src))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (workspace == nullptr) return IPUS_ERROR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(reduce_rows_block_major_kernel, dim3(rows / 16, kReduceSplits), dim3(kThreads),
+                     0, stream, workspace, (const uint16_t*)src, rows, columns, row_block,
+                     column_block);
+  hipLaunchKernelGGL(reduce_splits_kernel, dim3(ceil_div(rows, kThreads)), dim3(kThreads), 0,
+                     stream, dst, (const float*)workspace, rows);
+  return hip_status(hipGetLastError());
+}
+
+int launch_reduce_sum_f16(hipStream_t stream, void* dst, const void* initial, const void* remote,
+                          uint32_t remote_partials, uint32_t count) {
+  if (count % 8 != 0) return IPUS_ERROR_UNSUPPORTED_COUNT;
+  if (!aligned16(dst) || !aligned16(initial) || !aligned16(remote))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (count == 0) return 0;
+  hipLaunchKernelGGL(reduce_sum_f16_kernel, dim3(grid_for(count / 8)), dim3(kThreads), 0, stream,
+                     (uint16_t*)dst, (const uint16_t*)initial, (const uint16_t*)remote,
+                     remote_partials, count);
+  return hip_status(hipGetLastError());
+}
+
+int launch_gelu_f16(hipStream_t stream, void* dst, const void* src, uint64_t count) {
+  if (count == 0) return 0;
+  if (aligned16(dst) && aligned16(src))
+    hipLaunchKernelGGL(gelu_f16_kernel, dim3(grid_for(count / 8 + 1)), dim3(kThreads), 0, stream,
+                       (uint16_t*)dst, (const uint16_t*)src, count);
+  else
+    hipLaunchKernelGGL(gelu_f16_scalar_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream,
+                       (uint16_t*)dst, (const uint16_t*)src, count);
+  return hip_status(hipGetLastError());
+}
+
+int launch_fill_zero(hipStream_t stream, void* dst, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  if (!aligned16(dst)) return IPUS_ERROR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(bytes / 16 + 1)), dim3(kThreads), 0, stream,
+                     (uint8_t*)dst, bytes);
+  return hip_status(hipGetLastError());
+}
+
+int launch_cast_f32_to_f16(hipStream_t stream, void* dst, const void* src, uint64_t count) {
+  if (count == 0) return 0;
+  hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream,
+                     (uint16_t*)dst, (const float*)src, count);
+  return hip_status(hipGetLastError());
+}
+
+int launch_cast_f16_to_f32(hipStream_t stream, void* dst, const void* src, uint64_t count) {
+  if (count == 0) return 0;
+  hipLaunchKernelGGL(cast_f16_f32_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream,
+                     (float*)dst, (const uint16_t*)src, count);
+  return hip_status(hipGetLastError());
+}
+
+int launch_add(hipStream_t stream, const AddArgs& a) {
+  if (a.rank < 0 || a.rank > 6) return IPUS_ERROR_INVALID_ARGUMENT;
+  AddShape s;
+  s.rank = a.rank;
+  uint64_t total = 1;
+  for (int i = 0; i < a.rank; ++i) {
+    s.shape[i] = a.shape[i];
+    s.ls[i] = a.left_strides[i];
+    s.rs[i] = a.right_strides[i];
+    total *= a.shape[i];
+  }
+  if (total == 0) return 0;
+  if (a.precision == 1)
+    hipLaunchKernelGGL(add_kernel<uint16_t>, dim3(grid_for(total)), dim3(kThreads), 0, stream,
+                       (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right, s,
+                       total);
+  else if (a.precision == 2)
+    hipLaunchKernelGGL(add_kernel<float>, dim3(grid_for(total)), dim3(kThreads), 0, stream,
+                       (float*)a.out, (const float*)a.left, (const float*)a.right, s, total);
+  else
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  return hip_status(hipGetLastError());
+}
+
+int launch_split_heads(hipStream_t stream, void* dst, const void* src, uint32_t batch,
+                       uint32_t rows, uint32_t heads, uint32_t channels, uint32_t element_bytes) {
+  const uint64_t total = (uint64_t)batch * rows * heads * channels;
+  if (total == 0) return 0;
+  if (element_bytes == 2)
+    hipLaunchKernelGGL(split_heads_kernel<uint16_t>, dim3(grid_for(total)), dim3(kThreads), 0,
+                       stream, (uint16_t*)dst, (const uint16_t*)src, rows, heads, channels, total);
+  else if (element_bytes == 4)
+    hipLaunchKernelGGL(split_heads_kernel<uint32_t>, dim3(grid_for(total)), dim3(kThreads), 0,
+                       stream, (uint32_t*)dst, (const uint32_t*)src, rows, heads, channels, total);
+  else
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  return hip_status(hipGetLastError());
+}
+
+int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
+                            uint32_t row_block, uint32_t column_block, uint32_t matrices,
+                            uint32_t rows, uint32_t columns) {
+  if (source_order > kOrderBlockMajor) return IPUS_ERROR_UNAVAILABLE;
+  if (source_order == kOrderAmpLeft && columns % kMicro != 0) return IPUS_ERROR_INVALID_ARGUMENT;
+  if (source_order == kOrderAmpTransposedRight && (rows % kMicro != 0 || columns % kMicro != 0))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (source_order == kOrderBlockMajor &&
+      (row_block == 0 || column_block == 0 || row_block % kMicro != 0 || rows % row_block != 0 ||
+       columns % column_block != 0))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  const uint64_t total = (uint64_t)matrices * rows * columns;
+  if (total == 0) return 0;
+  if (source_order == kOrderBlockMajor && column_block % 8 == 0 && aligned16(dst) &&
+      aligned16(src) && matrices <= 65535) {
+    const uint32_t tiles_r = ceil_div(rows, 64), tiles_c = ceil_div(columns, 256);
+    hipLaunchKernelGGL(block_major_to_row_major_f16_kernel, dim3(tiles_r * tiles_c, matrices),
+                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src, rows,
+                       columns, row_block, column_block, tiles_c);
+  } else {
+    hipLaunchKernelGGL(to_row_major_f16_general_kernel, dim3(ceil_div(total, kThreads)),
+                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
+                       source_order, row_block, column_block, matrices, rows, columns, total);
+  }
+  return hip_status(hipGetLastError());
+}
+
+}  // namespace ipus

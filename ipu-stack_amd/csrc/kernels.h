@@ -1,0 +1,86 @@
+// Host-side launchers of the gfx950 kernels.  Each launcher validates the
+// shape it needs, picks a grid, and enqueues on the given stream.  They return
+// 0 or a negative ipus status (see include/ipus.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ipus {
+
+struct GemmArgs {
+  void* out;
+  const void* left;
+  const void* right;
+  uint32_t batches;
+  uint64_t left_batch_stride;   // elements; 0 broadcasts one matrix
+  uint64_t right_batch_stride;  // elements; 0 broadcasts one matrix
+  uint32_t rows, columns, inner;
+  bool transpose_left, transpose_right;
+};
+
+struct AttentionArgs {
+  void* out;
+  const void* query;
+  const void* key;
+  const void* value;
+  uint32_t streams, query_rows, key_rows, width, value_width;
+  float scale;
+  bool causal;
+  bool output_f16;  // false: fp32 output (reference), true: fp16
+};
+
+// Dense products (k_gemm_f16.hip, k_gemm_f32.hip).
+int launch_gemm_f16(hipStream_t stream, const GemmArgs& a);
+int launch_gemm_f32(hipStream_t stream, const GemmArgs& a);
+
+// Fused online-softmax attention (k_attention.hip).
+int launch_attention_f16(hipStream_t stream, const AttentionArgs& a);
+
+// Bandwidth kernels (k_memory.hip).
+int launch_transpose_f16(hipStream_t stream, void* dst, const void* src, uint32_t matrices,
+                         uint32_t rows, uint32_t columns);
+int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_t target_order,
+                         uint32_t row_block, uint32_t column_block, uint32_t matrices,
+                         uint32_t logical_rows, uint32_t physical_rows, uint32_t logical_columns,
+                         uint32_t physical_columns);
+int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
+                      uint32_t matrices, uint32_t logical_rows, uint32_t physical_rows,
+                      uint32_t logical_columns, uint32_t physical_columns);
+// Row sums with fp32 accumulation of a logical [rows, columns] fp16 matrix
+// stored row-major (source_order = 3) or block-major (source_order = 2).
+// `workspace` must hold reduce_rows_workspace_bytes(...) bytes.
+size_t reduce_rows_workspace_bytes(uint32_t source_order, uint32_t rows, uint32_t columns);
+int launch_reduce_rows_f16(hipStream_t stream, float* dst, const void* src, uint32_t source_order,
+                           uint32_t row_block, uint32_t column_block, uint32_t rows,
+                           uint32_t columns, float* workspace);
+int launch_reduce_sum_f16(hipStream_t stream, void* dst, const void* initial, const void* remote,
+                          uint32_t remote_partials, uint32_t count);
+int launch_gelu_f16(hipStream_t stream, void* dst, const void* src, uint64_t count);
+int launch_fill_zero(hipStream_t stream, void* dst, uint64_t bytes);
+int launch_cast_f32_to_f16(hipStream_t stream, void* dst, const void* src, uint64_t count);
+int launch_cast_f16_to_f32(hipStream_t stream, void* dst, const void* src, uint64_t count);
+// out = left + right with numpy broadcasting over up to 6 axes; strides are
+// in elements, 0 on broadcast axes.  precision: 1 = f16, 2 = f32.
+struct AddArgs {
+  void* out;
+  const void* left;
+  const void* right;
+  int rank;
+  uint32_t shape[6];
+  uint64_t left_strides[6];
+  uint64_t right_strides[6];
+  int precision;
+};
+int launch_add(hipStream_t stream, const AddArgs& a);
+// Streams = batch * heads: [batch, rows, heads*ch] -> [batch*heads, rows, ch];
+// element_bytes 2 or 4.
+int launch_split_heads(hipStream_t stream, void* dst, const void* src, uint32_t batch,
+                       uint32_t rows, uint32_t heads, uint32_t channels, uint32_t element_bytes);
+// Stored order (AmpLeft, AmpTransposedRight, BlockMajor) -> row-major.
+int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
+                            uint32_t row_block, uint32_t column_block, uint32_t matrices,
+                            uint32_t rows, uint32_t columns);
+
+}  // namespace ipus

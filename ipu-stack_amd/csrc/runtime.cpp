@@ -1,0 +1,641 @@
+// libipus host runtime: context, buffers, events, the kernel ABI registry and
+// ipus_launch, synthetic input generation.  C ABI in include/ipus.h.
+#include "../../include/ipus.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "internal.h"
+#include "kernels.h"
+
+namespace ipus {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buffer[1024];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buffer, sizeof(buffer), fmt, args);
+  va_end(args);
+  g_last_error = buffer;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(IPUS_ERROR_HIP_BASE - (int)e, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+int check_launch(int status, const char* symbol) {
+  if (status == 0) return 0;
+  if (status <= IPUS_ERROR_HIP_BASE)
+    return fail(status, "%s: launch failed: %s", symbol,
+                hipGetErrorString((hipError_t)(IPUS_ERROR_HIP_BASE - status)));
+  switch (status) {
+    case IPUS_ERROR_UNAVAILABLE:
+      return fail(status, "kernel %s has no device implementation for these arguments", symbol);
+    case IPUS_ERROR_UNSUPPORTED_COUNT:
+      return fail(status, "kernel %s does not support this element count", symbol);
+    default:
+      return fail(status, "kernel %s rejected its arguments", symbol);
+  }
+}
+
+}  // namespace ipus
+
+using namespace ipus;
+
+float* ipus_context::workspace(size_t bytes) {
+  if (bytes == 0) return nullptr;
+  if (bytes > workspace_bytes) {
+    if (workspace_ptr) {
+      hipStreamSynchronize(stream);
+      hipFree(workspace_ptr);
+      workspace_ptr = nullptr;
+      workspace_bytes = 0;
+    }
+    if (hipMalloc(&workspace_ptr, bytes) != hipSuccess) return nullptr;
+    workspace_bytes = bytes;
+  }
+  return (float*)workspace_ptr;
+}
+
+
+// ---------------------------------------------------------------------------
+// Errors, version
+// ---------------------------------------------------------------------------
+extern "C" const char* ipus_last_error(void) { return g_last_error.c_str(); }
+extern "C" const char* ipus_version(void) { return "libipus 0.1.0 (gfx950)"; }
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+extern "C" int ipus_device_count(int* count) {
+  if (!count) return fail(IPUS_ERROR_INVALID_ARGUMENT, "count is null");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice) {
+    *count = 0;
+    return 0;
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  *count = n;
+  return 0;
+}
+
+extern "C" int ipus_context_create(int device, ipus_context** out) {
+  if (!out) return fail(IPUS_ERROR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return fail(IPUS_ERROR_NO_DEVICE, "no HIP device is available (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, n);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  auto* ctx = new ipus_context();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  *out = ctx;
+  return 0;
+}
+
+extern "C" int ipus_context_destroy(ipus_context* ctx) {
+  if (!ctx) return 0;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  if (ctx->workspace_ptr) hipFree(ctx->workspace_ptr);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return 0;
+}
+
+extern "C" int ipus_context_device_info(ipus_context* ctx, ipus_device_info* info) {
+  if (!ctx || !info) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, ctx->device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  memset(info, 0, sizeof(*info));
+  snprintf(info->name, sizeof(info->name), "%s", p.name);
+  snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
+  info->compute_units = p.multiProcessorCount;
+  info->clock_khz = p.clockRate;
+  info->memory_clock_khz = p.memoryClockRate;
+  info->memory_bus_width = p.memoryBusWidth;
+  info->global_memory_bytes = p.totalGlobalMem;
+  info->lds_bytes_per_block = (int)p.sharedMemPerBlock;
+  return 0;
+}
+
+extern "C" int ipus_context_stream(ipus_context* ctx, void** stream) {
+  if (!ctx || !stream) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  *stream = (void*)ctx->stream;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Buffers
+// ---------------------------------------------------------------------------
+extern "C" int ipus_buffer_alloc(ipus_context* ctx, size_t bytes, void** ptr) {
+  if (!ctx || !ptr) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  hipSetDevice(ctx->device);
+  // 256-byte aligned by hipMalloc; zero-byte requests get a valid pointer.
+  hipError_t e = hipMalloc(ptr, bytes ? bytes : 256);
+  if (e == hipErrorOutOfMemory)
+    return fail(IPUS_ERROR_OUT_OF_MEMORY, "out of device memory allocating %zu bytes", bytes);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  return 0;
+}
+
+extern "C" int ipus_buffer_free(ipus_context* ctx, void* ptr) {
+  if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
+  if (!ptr) return 0;
+  hipSetDevice(ctx->device);
+  hipError_t e = hipFree(ptr);
+  if (e != hipSuccess) return hip_fail(e, "hipFree");
+  return 0;
+}
+
+extern "C" int ipus_buffer_upload(ipus_context* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes))
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (!bytes) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "upload");
+  return 0;
+}
+
+extern "C" int ipus_buffer_download(ipus_context* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes))
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (!bytes) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "download");
+  return 0;
+}
+
+extern "C" int ipus_buffer_copy(ipus_context* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes))
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (!bytes) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "copy");
+  return 0;
+}
+
+extern "C" int ipus_buffer_memset(ipus_context* ctx, void* ptr, int value, size_t bytes) {
+  if (!ctx || (!ptr && bytes)) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (!bytes) return 0;
+  hipError_t e = hipMemsetAsync(ptr, value, bytes, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "memset");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Sync and events
+// ---------------------------------------------------------------------------
+struct ipus_event {
+  hipEvent_t event;
+};
+
+extern "C" int ipus_stream_sync(ipus_context* ctx) {
+  if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  return 0;
+}
+
+extern "C" int ipus_event_create(ipus_context* ctx, ipus_event** out) {
+  if (!ctx || !out) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  hipSetDevice(ctx->device);
+  auto* ev = new ipus_event();
+  hipError_t e = hipEventCreate(&ev->event);
+  if (e != hipSuccess) {
+    delete ev;
+    return hip_fail(e, "hipEventCreate");
+  }
+  *out = ev;
+  return 0;
+}
+
+extern "C" int ipus_event_destroy(ipus_event* ev) {
+  if (!ev) return 0;
+  hipEventDestroy(ev->event);
+  delete ev;
+  return 0;
+}
+
+extern "C" int ipus_event_record(ipus_context* ctx, ipus_event* ev) {
+  if (!ctx || !ev) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  hipError_t e = hipEventRecord(ev->event, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+  return 0;
+}
+
+extern "C" int ipus_event_elapsed_ms(ipus_event* start, ipus_event* end, float* ms) {
+  if (!start || !end || !ms) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  hipError_t e = hipEventSynchronize(end->event);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, start->event, end->event);
+  if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel ABI registry and launch (tile_kernel_abi / validate_kernel_run /
+// ComputeStep, crates/ipu-codegen/src/kernel.rs:1215-1435, 818-865).
+// ---------------------------------------------------------------------------
+namespace {
+
+using Launcher = int (*)(ipus_context*, void*, const void* const*, const uint32_t*);
+
+struct KernelEntry {
+  const char* symbol;
+  int inputs;
+  std::vector<const char*> scalars;
+  Launcher launch;
+};
+
+inline float bits_to_float(uint32_t bits) {
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+int run_gemm(ipus_context* ctx, void* out, const void* const* in, const uint32_t* s, bool f16) {
+  GemmArgs a;
+  a.out = out;
+  a.left = in[0];
+  a.right = in[1];
+  a.batches = s[0];
+  a.rows = s[1];
+  a.columns = s[2];
+  a.inner = s[3];
+  a.transpose_left = s[4] != 0;
+  a.transpose_right = s[5] != 0;
+  a.left_batch_stride = s[6];
+  a.right_batch_stride = s[7];
+  if (s[4] > 1 || s[5] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+  return f16 ? launch_gemm_f16(ctx->stream, a) : launch_gemm_f32(ctx->stream, a);
+}
+
+const std::vector<KernelEntry>& registry() {
+  static const std::vector<KernelEntry> entries = {
+      {"ipu_stack_gemm_f16", 2,
+       {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
+        "left_batch_stride", "right_batch_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_gemm(c, o, i, s, true);
+       }},
+      {"ipu_stack_gemm_f32", 2,
+       {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
+        "left_batch_stride", "right_batch_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_gemm(c, o, i, s, false);
+       }},
+      {"ipu_stack_flash_attention_online_f16", 3,
+       {"matrices", "query_rows", "key_rows", "query_dimension", "value_dimension", "scale_bits",
+        "causal", "output_f16"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         AttentionArgs a;
+         a.out = o;
+         a.query = i[0];
+         a.key = i[1];
+         a.value = i[2];
+         a.streams = s[0];
+         a.query_rows = s[1];
+         a.key_rows = s[2];
+         a.width = s[3];
+         a.value_width = s[4];
+         a.scale = s[5] == 0 ? 1.0f / std::sqrt((float)s[3]) : bits_to_float(s[5]);
+         a.causal = s[6] != 0;
+         a.output_f16 = s[7] != 0;
+         if (s[6] > 1 || s[7] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+         return launch_attention_f16(c->stream, a);
+       }},
+      {"ipu_stack_gelu_tanh_approx_f16", 1, {"element_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         // validate_kernel_run: the element count must be even (kernel.rs:1400-1413).
+         if (s[0] % 2 != 0) return IPUS_ERROR_UNSUPPORTED_COUNT;
+         return launch_gelu_f16(c->stream, o, i[0], s[0]);
+       }},
+      {"ipu_stack_reduce_sum_f16", 2, {"num_partials", "element_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         // partials >= 2 (one initial + >= 1 remote) and count % 8 == 0
+         // (kernel.rs:1414-1423).
+         if (s[0] < 1 || s[1] % 8 != 0) return IPUS_ERROR_UNSUPPORTED_COUNT;
+         return launch_reduce_sum_f16(c->stream, o, i[0], i[1], s[0], s[1]);
+       }},
+      {"ipu_stack_rearrange_row_major_f16", 1,
+       {"logical_rows", "physical_rows", "target_order", "logical_columns", "physical_columns",
+        "row_block", "column_block", "matrices"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_rearrange_f16(c->stream, o, i[0], s[2], s[5], s[6], s[7], s[0], s[1], s[3],
+                                     s[4]);
+       }},
+      {"ipu_stack_unpack_amp_f16", 1,
+       {"matrices", "logical_rows", "physical_rows", "logical_columns", "physical_columns",
+        "source_order"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_unpack_f16(c->stream, o, i[0], s[5], s[0], s[1], s[2], s[3], s[4]);
+       }},
+      {"ipu_stack_transpose_f16", 1, {"matrices", "rows", "columns"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_transpose_f16(c->stream, o, i[0], s[0], s[1], s[2]);
+       }},
+      {"ipu_stack_reduce_rows_f16", 1,
+       {"rows", "columns", "source_order", "row_block", "column_block"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         float* ws = nullptr;
+         const size_t bytes = reduce_rows_workspace_bytes(s[2], s[0], s[1]);
+         if (bytes) {
+           ws = c->workspace(bytes);
+           if (!ws) return IPUS_ERROR_OUT_OF_MEMORY;
+         }
+         return launch_reduce_rows_f16(c->stream, (float*)o, i[0], s[2], s[3], s[4], s[0], s[1],
+                                       ws);
+       }},
+      {"ipu_stack_fill_zero", 0, {"byte_count"},
+       [](ipus_context* c, void* o, const void* const*, const uint32_t* s) {
+         return launch_fill_zero(c->stream, o, s[0]);
+       }},
+      {"ipu_stack_cast_f32_f16", 1, {"element_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_cast_f32_to_f16(c->stream, o, i[0], s[0]);
+       }},
+      {"ipu_stack_cast_f16_f32", 1, {"element_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_cast_f16_to_f32(c->stream, o, i[0], s[0]);
+       }},
+      {"ipu_stack_add_f16", 2, {"element_count", "left_broadcast_stride", "right_broadcast_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_flat_add(c, o, i, s, 1);
+       }},
+      {"ipu_stack_add_f32", 2, {"element_count", "left_broadcast_stride", "right_broadcast_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_flat_add(c, o, i, s, 2);
+       }},
+      // Plan-internal symbols (no reference counterpart): general numpy
+      // broadcasting add, split_heads copy, stored order -> row-major, GELU
+      // of any element count, byte copy.
+      {"ipu_stack_add_broadcast_f16", 2,
+       {"rank", "shape0", "shape1", "shape2", "shape3", "shape4", "shape5", "left_stride0",
+        "left_stride1", "left_stride2", "left_stride3", "left_stride4", "left_stride5",
+        "right_stride0", "right_stride1", "right_stride2", "right_stride3", "right_stride4",
+        "right_stride5"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_broadcast_add(c, o, i, s, 1);
+       }},
+      {"ipu_stack_add_broadcast_f32", 2,
+       {"rank", "shape0", "shape1", "shape2", "shape3", "shape4", "shape5", "left_stride0",
+        "left_stride1", "left_stride2", "left_stride3", "left_stride4", "left_stride5",
+        "right_stride0", "right_stride1", "right_stride2", "right_stride3", "right_stride4",
+        "right_stride5"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_broadcast_add(c, o, i, s, 2);
+       }},
+      {"ipu_stack_split_heads", 1, {"batch", "rows", "heads", "channels", "element_bytes"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_split_heads(c->stream, o, i[0], s[0], s[1], s[2], s[3], s[4]);
+       }},
+      {"ipu_stack_rearrange_to_row_major_f16", 1,
+       {"source_order", "row_block", "column_block", "matrices", "rows", "columns"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_to_row_major_f16(c->stream, o, i[0], s[0], s[1], s[2], s[3], s[4], s[5]);
+       }},
+      {"ipus_gelu_f16", 1, {"element_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_gelu_f16(c->stream, o, i[0], s[0]);
+       }},
+      {"ipu_stack_copy", 1, {"byte_count"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         if (s[0] == 0) return 0;
+         const hipError_t e = hipMemcpyAsync(o, i[0], s[0], hipMemcpyDeviceToDevice, c->stream);
+         return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e;
+       }},
+  };
+  return entries;
+}
+
+const KernelEntry* find_kernel(const char* symbol) {
+  if (!symbol) return nullptr;
+  for (const auto& e : registry())
+    if (strcmp(e.symbol, symbol) == 0) return &e;
+  return nullptr;
+}
+
+void fill_info(const KernelEntry& e, ipus_kernel_abi_info* info) {
+  memset(info, 0, sizeof(*info));
+  info->symbol = e.symbol;
+  info->input_count = e.inputs;
+  info->scalar_count = (int)e.scalars.size();
+  for (size_t k = 0; k < e.scalars.size() && k < IPUS_MAX_SCALARS; ++k)
+    info->scalar_names[k] = e.scalars[k];
+  info->implemented = 1;
+}
+
+}  // namespace
+
+namespace ipus {
+// out[i] = left[i % L] + right[i % R] with L, R the broadcast strides (operand
+// element counts; each must divide the element count).
+int run_flat_add(ipus_context* c, void* o, const void* const* i, const uint32_t* s, int precision) {
+  const uint32_t count = s[0], L = s[1], R = s[2];
+  if (L == 0 || R == 0 || count % L != 0 || count % R != 0) return IPUS_ERROR_INVALID_ARGUMENT;
+  AddArgs a;
+  a.out = o;
+  a.left = i[0];
+  a.right = i[1];
+  a.precision = precision;
+  // Express as a 3-axis broadcast: [count / max, max / min, min] handled by
+  // two views, each operand repeating with its own period.
+  if (L == R) {
+    a.rank = 2;
+    a.shape[0] = count / L;
+    a.shape[1] = L;
+    a.left_strides[0] = 0;
+    a.left_strides[1] = 1;
+    a.right_strides[0] = 0;
+    a.right_strides[1] = 1;
+  } else {
+    const uint32_t big = L > R ? L : R, small = L > R ? R : L;
+    if (big % small != 0) return IPUS_ERROR_INVALID_ARGUMENT;
+    a.rank = 3;
+    a.shape[0] = count / big;
+    a.shape[1] = big / small;
+    a.shape[2] = small;
+    const bool left_big = L > R;
+    a.left_strides[0] = 0;
+    a.left_strides[1] = left_big ? small : 0;
+    a.left_strides[2] = 1;
+    a.right_strides[0] = 0;
+    a.right_strides[1] = left_big ? 0 : small;
+    a.right_strides[2] = 1;
+  }
+  return launch_add(c->stream, a);
+}
+
+// Scalars: rank, shape[6], left strides[6], right strides[6] (elements).
+int run_broadcast_add(ipus_context* c, void* o, const void* const* i, const uint32_t* s,
+                      int precision) {
+  AddArgs a;
+  a.out = o;
+  a.left = i[0];
+  a.right = i[1];
+  a.precision = precision;
+  a.rank = (int)s[0];
+  if (a.rank < 0 || a.rank > 6) return IPUS_ERROR_INVALID_ARGUMENT;
+  for (int k = 0; k < 6; ++k) {
+    a.shape[k] = s[1 + k];
+    a.left_strides[k] = s[7 + k];
+    a.right_strides[k] = s[13 + k];
+  }
+  return launch_add(c->stream, a);
+}
+}  // namespace ipus
+
+extern "C" int ipus_kernel_count(int* count) {
+  if (!count) return fail(IPUS_ERROR_INVALID_ARGUMENT, "count is null");
+  *count = (int)registry().size();
+  return 0;
+}
+
+extern "C" int ipus_kernel_abi_at(int index, ipus_kernel_abi_info* info) {
+  if (!info || index < 0 || index >= (int)registry().size())
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel index %d out of range", index);
+  fill_info(registry()[(size_t)index], info);
+  return 0;
+}
+
+extern "C" int ipus_kernel_abi(const char* symbol, ipus_kernel_abi_info* info) {
+  if (!info) return fail(IPUS_ERROR_INVALID_ARGUMENT, "info is null");
+  const KernelEntry* e = find_kernel(symbol);
+  if (!e) return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "unknown kernel symbol %s", symbol ? symbol : "(null)");
+  fill_info(*e, info);
+  return 0;
+}
+
+extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
+                           const void* const* inputs, int input_count, const uint32_t* scalars,
+                           int scalar_count) {
+  if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
+  const KernelEntry* e = find_kernel(symbol);
+  if (!e) return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "unknown kernel symbol %s", symbol ? symbol : "(null)");
+  if (input_count != e->inputs)
+    return fail(IPUS_ERROR_POINTER_ARITY, "kernel run has %d pointer operands, ABI requires %d",
+                input_count, e->inputs);
+  if (scalar_count != (int)e->scalars.size())
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s takes %d scalars, got %d", symbol,
+                (int)e->scalars.size(), scalar_count);
+  if (!output) return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null output", symbol);
+  for (int k = 0; k < input_count; ++k)
+    if (!inputs || !inputs[k])
+      return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null input %d", symbol, k);
+  if (scalar_count && !scalars) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null scalars");
+  hipSetDevice(ctx->device);
+  return check_launch(e->launch(ctx, output, inputs, scalars), symbol);
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic inputs
+// ---------------------------------------------------------------------------
+namespace {
+
+inline uint64_t splitmix64(uint64_t state) {
+  uint64_t z = state + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+inline float synth_value(uint64_t seed, uint32_t tensor, uint64_t i, int dist, float scale) {
+  const uint64_t z = splitmix64(seed ^ ((uint64_t)tensor << 48) ^ i);
+  if (dist == 0) {
+    // top 24 bits -> [-1, 1)
+    const double u = (double)(z >> 40) * (1.0 / 16777216.0);
+    return (float)(2.0 * u - 1.0) * scale;
+  }
+  // Box-Muller with u1 in (0, 1] from the high 32 bits, u2 from the low 32.
+  const double u1 = ((double)(z >> 32) + 1.0) * (1.0 / 4294967296.0);
+  const double u2 = (double)(z & 0xffffffffu) * (1.0 / 4294967296.0);
+  const double r = std::sqrt(-2.0 * std::log(u1));
+  return (float)(r * std::cos(6.283185307179586 * u2)) * scale;
+}
+
+uint16_t f32_to_f16_rne(float value) {
+  uint32_t x;
+  memcpy(&x, &value, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t exponent = (x >> 23) & 0xffu;
+  uint32_t mantissa = x & 0x7fffffu;
+  if (exponent == 0xffu) return (uint16_t)(sign | 0x7c00u | (mantissa ? 0x200u : 0u));
+  const int32_t e = (int32_t)exponent - 112;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    mantissa |= 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    uint32_t r = mantissa >> shift;
+    const uint32_t rem = mantissa & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+  }
+  uint32_t r = ((uint32_t)e << 10) | (mantissa >> 13);
+  const uint32_t rem = mantissa & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+  return (uint16_t)(sign | r);
+}
+
+template <typename F>
+void parallel_chunks(uint64_t count, F&& f) {
+  unsigned threads = std::thread::hardware_concurrency();
+  if (threads == 0) threads = 1;
+  if (threads > 16) threads = 16;
+  if (count < (1u << 16)) threads = 1;
+  std::vector<std::thread> pool;
+  for (unsigned t = 0; t < threads; ++t)
+    pool.emplace_back([&, t] { f(count * t / threads, count * (t + 1) / threads); });
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" int ipus_synth_f16(uint16_t* out, uint64_t count, uint64_t seed, uint32_t tensor,
+                              int distribution, float scale) {
+  if (!out && count) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null output");
+  if (distribution != 0 && distribution != 1)
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "distribution must be 0 (uniform) or 1 (normal)");
+  parallel_chunks(count, [&](uint64_t b, uint64_t e) {
+    for (uint64_t i = b; i < e; ++i)
+      out[i] = f32_to_f16_rne(synth_value(seed, tensor, i, distribution, scale));
+  });
+  return 0;
+}
+
+extern "C" int ipus_synth_f32(float* out, uint64_t count, uint64_t seed, uint32_t tensor,
+                              int distribution, float scale) {
+  if (!out && count) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null output");
+  if (distribution != 0 && distribution != 1)
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "distribution must be 0 (uniform) or 1 (normal)");
+  parallel_chunks(count, [&](uint64_t b, uint64_t e) {
+    for (uint64_t i = b; i < e; ++i) out[i] = synth_value(seed, tensor, i, distribution, scale);
+  });
+  return 0;
+}

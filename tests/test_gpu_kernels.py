@@ -1,0 +1,361 @@
+"""GPU parity of every hot-path kernel against the CPU oracle, through the C ABI
+(ipus_launch).  Bars: bit-exact for rearranges / transposes / the reference's
+fp16 partial-sum reduction; normwise max-rel <= 1e-2 for fp16 results
+(BASELINE.json north_star); fp32 results <= 1e-5."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+
+FP16_TOL = 1e-2   # north_star: max relative error <= 1e-2 vs fp32-accumulate
+FP32_TOL = 1e-5
+
+
+def synth(ipus, n, seed, tensor, dist=0, scale=1.0):
+    return ipus.synth_f16(n, seed, tensor, dist, scale)
+
+
+def run(ctx, symbol, out_nbytes, inputs, scalars, dtype=np.uint16):
+    bufs = [ctx.upload(x) for x in inputs]
+    out = ctx.alloc(out_nbytes)
+    ctx.launch(symbol, out, bufs, scalars)
+    result = out.download(dtype)
+    for b in bufs:
+        b.free()
+    out.free()
+    return result
+
+
+# ---------------------------------------------------------------------------
+# Transpose and rearranges (bit-exact)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("matrices,rows,cols", [
+    (1, 64, 64), (3, 128, 256), (1, 1000, 24), (2, 17, 33), (1, 8, 4096), (1, 8192, 8192)])
+def test_transpose_bit_exact(ipus, oracle, ctx, matrices, rows, cols):
+    x = synth(ipus, matrices * rows * cols, 11, 1, 1)
+    got = run(ctx, "ipu_stack_transpose_f16", x.nbytes, [x], [matrices, rows, cols])
+    assert np.array_equal(got, oracle.transpose_u16(x, matrices, rows, cols))
+
+
+@pytest.mark.parametrize("rows,cols,rb,cb", [
+    (64, 16, 64, 16), (64, 64, 64, 64), (256, 512, 64, 16), (128, 192, 64, 64),
+    (96, 48, 32, 16), (8192, 8192, 64, 64), (8192, 8192, 64, 16)])
+def test_block_major_bit_exact(ipus, oracle, ctx, rows, cols, rb, cb):
+    x = synth(ipus, rows * cols, 12, 2, 1)
+    got = run(ctx, "ipu_stack_rearrange_row_major_f16", x.nbytes, [x],
+              [rows, rows, ipus.ORDER_BLOCK_MAJOR, cols, cols, rb, cb, 1])
+    want = oracle.rearrange_row_major_f16(x, 2, 1, rows, rows, cols, cols, rb, cb)
+    assert np.array_equal(got, want)
+    # and back to row-major
+    back = run(ctx, "ipu_stack_rearrange_to_row_major_f16", x.nbytes, [got],
+               [ipus.ORDER_BLOCK_MAJOR, rb, cb, 1, rows, cols])
+    assert np.array_equal(back, x)
+
+
+@pytest.mark.parametrize("order", [0, 1, 2])
+@pytest.mark.parametrize("matrices,lr,pr,lc,pc", [
+    (1, 64, 64, 16, 16), (2, 50, 64, 40, 48), (3, 17, 32, 30, 32), (1, 64, 64, 64, 64)])
+def test_rearrange_with_padding_bit_exact(ipus, oracle, ctx, order, matrices, lr, pr, lc, pc):
+    x = synth(ipus, matrices * lr * lc, 13, 3, 1)
+    got = run(ctx, "ipu_stack_rearrange_row_major_f16", matrices * pr * pc * 2, [x],
+              [lr, pr, order, lc, pc, 32, 16, matrices])
+    want = oracle.rearrange_row_major_f16(x, order, matrices, lr, pr, lc, pc, 32, 16)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("source", [0, 1])
+@pytest.mark.parametrize("matrices,lr,pr,lc,pc", [
+    (1, 16, 16, 16, 16), (2, 30, 32, 40, 48), (1, 64, 64, 64, 64)])
+def test_unpack_bit_exact(ipus, oracle, ctx, source, matrices, lr, pr, lc, pc):
+    x = synth(ipus, matrices * pr * pc, 14, 4, 1)
+    got = run(ctx, "ipu_stack_unpack_amp_f16", x.nbytes, [x], [matrices, lr, pr, lc, pc, source])
+    want = oracle.unpack_to_row_major_f16(x, source, matrices, lr, pr, lc, pc)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# Reductions
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(1, 8), (3, 1000), (64, 4096), (5, 37), (8192, 8192)])
+def test_reduce_rows_row_major(ipus, oracle, ctx, rows, cols):
+    x = synth(ipus, rows * cols, 15, 5, 1)
+    got = run(ctx, "ipu_stack_reduce_rows_f16", rows * 4, [x], [rows, cols, 3, 0, 0], np.float32)
+    want = oracle.reduce_rows_f16(x, rows, cols)
+    assert max_rel(got, want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("rows,cols,rb,cb", [(64, 64, 64, 64), (128, 256, 64, 16),
+                                             (8192, 8192, 64, 64)])
+def test_reduce_rows_block_major(ipus, oracle, ctx, rows, cols, rb, cb):
+    x = synth(ipus, rows * cols, 16, 6, 1)
+    bm = oracle.rearrange_row_major_f16(x, 2, 1, rows, rows, cols, cols, rb, cb)
+    got = run(ctx, "ipu_stack_reduce_rows_f16", rows * 4, [bm], [rows, cols, 2, rb, cb],
+              np.float32)
+    want = oracle.reduce_rows_f16(x, rows, cols)
+    assert max_rel(got, want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("partials,count", [(1, 8), (3, 1024), (7, 4096), (1, 1 << 20)])
+def test_reduce_sum_f16_bit_exact(ipus, oracle, ctx, partials, count):
+    initial = synth(ipus, count, 17, 7, 1)
+    remote = synth(ipus, partials * count, 17, 8, 1)
+    got = run(ctx, "ipu_stack_reduce_sum_f16", count * 2, [initial, remote], [partials, count])
+    assert np.array_equal(got, oracle.reduce_sum_f16(initial, remote, partials, count))
+
+
+def test_reduce_sum_f16_rejects_reference_invalid_counts(ipus, ctx):
+    buf = ctx.alloc(64)
+    with pytest.raises(ipus.KernelAbiError) as e:
+        ctx.launch("ipu_stack_reduce_sum_f16", buf, [buf, buf], [1, 12])  # count % 8 != 0
+    assert e.value.status == ipus.ERROR_UNSUPPORTED_COUNT
+    with pytest.raises(ipus.KernelAbiError):
+        ctx.launch("ipu_stack_reduce_sum_f16", buf, [buf, buf], [0, 8])   # partials < 2
+    buf.free()
+
+
+# ---------------------------------------------------------------------------
+# GELU
+# ---------------------------------------------------------------------------
+def ulp_distance(a, b):
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    # map sign-magnitude to a monotonic integer line
+    a = np.where(a & 0x8000, -(a & 0x7FFF), a)
+    b = np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(a - b)
+
+
+def test_gelu_every_fp16_input(ipus, oracle, ctx):
+    """All 65536 fp16 bit patterns (NaNs compared as NaN)."""
+    x = np.arange(65536, dtype=np.uint16)
+    got = run(ctx, "ipu_stack_gelu_tanh_approx_f16", x.nbytes, [x], [x.size])
+    want = oracle.gelu_f16(x)
+    gf, wf = oracle.f16_to_f32(got), oracle.f16_to_f32(want)
+    xf = oracle.f16_to_f32(x)
+    nan = np.isnan(wf)
+    assert np.array_equal(np.isnan(gf), nan)
+    assert np.array_equal(gf[np.isinf(wf)], wf[np.isinf(wf)])
+    # |x| <= 4: both evaluations are accurate to well under an fp16 ulp.
+    core = ~nan & (np.abs(xf) <= 4)
+    d = ulp_distance(got[core], want[core])
+    assert d.max() <= 1, f"max ulp distance {d.max()}"
+    assert np.mean(d == 0) >= 0.99
+    # Far tail: the reference's f32 1 + tanh(u) cancels; values are tiny.
+    tail = np.isfinite(wf) & (np.abs(xf) > 4)
+    assert np.max(np.abs(gf[tail] - wf[tail])) <= 1e-6
+    finite = np.isfinite(wf)
+    assert max_rel(gf[finite], wf[finite]) <= 1e-3
+
+
+@pytest.mark.parametrize("count", [2, 130, 4096 * 16384])
+def test_gelu_sizes(ipus, oracle, ctx, count):
+    x = synth(ipus, count, 18, 9, 1, 2.0)
+    got = run(ctx, "ipu_stack_gelu_tanh_approx_f16", x.nbytes, [x], [count])
+    want = oracle.gelu_f16(x)
+    core = np.abs(oracle.f16_to_f32(x)) <= 4
+    assert ulp_distance(got[core], want[core]).max() <= 1
+    assert max_rel(oracle.f16_to_f32(got), oracle.f16_to_f32(want)) <= 1e-3
+
+
+def test_gelu_rejects_odd_count(ipus, ctx):
+    buf = ctx.alloc(64)
+    with pytest.raises(ipus.KernelAbiError) as e:
+        ctx.launch("ipu_stack_gelu_tanh_approx_f16", buf, [buf], [7])
+    assert e.value.status == ipus.ERROR_UNSUPPORTED_COUNT
+    buf.free()
+
+
+# ---------------------------------------------------------------------------
+# fp16 GEMM
+# ---------------------------------------------------------------------------
+def gemm_case(ipus, oracle, ctx, M, N, K, tl=False, tr=False, batches=1, bl=True, br=True,
+              seed=19):
+    lcount = batches if bl else 1
+    rcount = batches if br else 1
+    a = synth(ipus, lcount * M * K, seed, 10)
+    b = synth(ipus, rcount * K * N, seed, 11)
+    got = run(ctx, "ipu_stack_gemm_f16", batches * M * N * 2, [a, b],
+              [batches, M, N, K, int(tl), int(tr), M * K if bl else 0, K * N if br else 0])
+    want = oracle.gemm_f16(a, b, M, N, K, tl, tr, batches, M * K if bl else 0,
+                           K * N if br else 0)
+    return oracle.f16_to_f32(got), oracle.f16_to_f32(want)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (512, 768, 320), (256, 512, 64),
+                                   (17, 19, 72), (1, 1, 1), (300, 200, 100), (1024, 1024, 1024)])
+def test_gemm_f16_shapes(ipus, oracle, ctx, M, N, K):
+    got, want = gemm_case(ipus, oracle, ctx, M, N, K)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+@pytest.mark.parametrize("tl", [False, True])
+@pytest.mark.parametrize("tr", [False, True])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 128), (100, 60, 40)])
+def test_gemm_f16_transposes(ipus, oracle, ctx, tl, tr, M, N, K):
+    got, want = gemm_case(ipus, oracle, ctx, M, N, K, tl, tr)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+@pytest.mark.parametrize("bl,br", [(True, True), (True, False), (False, True)])
+def test_gemm_f16_batched_broadcast(ipus, oracle, ctx, bl, br):
+    got, want = gemm_case(ipus, oracle, ctx, 256, 256, 128, batches=3, bl=bl, br=br)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+def test_gemm_f16_one_hot_kat_bit_exact(ipus, oracle, ctx):
+    """crates/ipu-tests/src/main.rs:1079-1105, 2077-2136: a one-hot left operand
+    selects rows of a 5-level right operand, so every output is exact."""
+    M, K, N = 512, 64, 512
+    levels = np.array([0xBC00, 0xB800, 0x0000, 0x3800, 0x3C00], dtype=np.uint16)
+    left = np.zeros((M, K), dtype=np.uint16)
+    selected = (np.arange(M) * 7) % 64
+    left[np.arange(M), selected] = 0x3C00
+    inner = np.arange(K)[:, None]
+    col = np.arange(N)[None, :]
+    right = levels[(inner * 3 + col) % 5]
+    got = run(ctx, "ipu_stack_gemm_f16", M * N * 2, [left, right], [1, M, N, K, 0, 0, 0, 0])
+    assert np.array_equal(got.reshape(M, N), right[selected])
+
+
+def test_gemm_f16_constant_kat(ipus, ctx, oracle):
+    """main.rs:1590-1591, 1774-1800: 1.0 x 0.25 -> K * 0.25 within 0.002|e| + 0.01."""
+    M = N = 512
+    K = 1024
+    left = np.full(M * K, 0x3C00, dtype=np.uint16)
+    right = np.full(K * N, 0x3400, dtype=np.uint16)
+    got = oracle.f16_to_f32(run(ctx, "ipu_stack_gemm_f16", M * N * 2, [left, right],
+                                [1, M, N, K, 0, 0, 0, 0]))
+    expected = K * 0.25
+    assert np.max(np.abs(got - expected)) <= 0.002 * expected + 0.01
+
+
+def test_gemm_f16_8192_sampled_rows(ipus, oracle, ctx):
+    """BASELINE config 2b at full size: 64 evenly sampled rows (diagnostic.rs:259-267)."""
+    n = 8192
+    a = synth(ipus, n * n, 2024, 1)
+    b = synth(ipus, n * n, 2024, 2)
+    got = run(ctx, "ipu_stack_gemm_f16", n * n * 2, [a, b], [1, n, n, n, 0, 0, 0, 0])
+    rows = np.array([i * (n - 1) // 63 for i in range(64)], dtype=np.uint32)
+    want = oracle.gemm_f16_rows(a, b, n, n, n, rows)
+    got_rows = oracle.f16_to_f32(got.reshape(n, n)[rows])
+    assert max_rel(got_rows, want) <= FP16_TOL
+
+
+# ---------------------------------------------------------------------------
+# fp32 GEMM
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,tl,tr", [(128, 128, 32, False, False), (256, 384, 96, False, False),
+                                         (128, 256, 64, True, False), (128, 256, 64, False, True),
+                                         (128, 256, 64, True, True), (33, 17, 9, False, False),
+                                         (65, 130, 70, True, True)])
+def test_gemm_f32(ipus, oracle, ctx, M, N, K, tl, tr):
+    a = ipus.synth_f32(M * K, 31, 1, 1)
+    b = ipus.synth_f32(K * N, 31, 2, 1)
+    got = run(ctx, "ipu_stack_gemm_f32", M * N * 4, [a, b], [1, M, N, K, int(tl), int(tr), 0, 0],
+              np.float32)
+    A = a.reshape((K, M) if tl else (M, K)).astype(np.float64)
+    B = b.reshape((N, K) if tr else (K, N)).astype(np.float64)
+    want = (A.T if tl else A) @ (B.T if tr else B)
+    assert max_rel(got.reshape(M, N), want) <= FP32_TOL
+
+
+def test_gemm_f32_4096_sampled_rows(ipus, ctx):
+    """BASELINE config 2a at full size, 32 sampled rows against an fp64 product."""
+    n = 4096
+    a = ipus.synth_f32(n * n, 4096, 1, 1)
+    b = ipus.synth_f32(n * n, 4096, 2, 1)
+    got = run(ctx, "ipu_stack_gemm_f32", n * n * 4, [a, b], [1, n, n, n, 0, 0, 0, 0], np.float32)
+    rows = np.array([i * (n - 1) // 31 for i in range(32)])
+    want = a.reshape(n, n)[rows].astype(np.float64) @ b.reshape(n, n).astype(np.float64)
+    assert max_rel(got.reshape(n, n)[rows], want) <= FP32_TOL
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal, scale=None, out_f16=False,
+                   rows=None, seed=41):
+    q = synth(ipus, streams * sq * d, seed, 1, 1)
+    k = synth(ipus, streams * sk * d, seed, 2, 1)
+    v = synth(ipus, streams * sk * dv, seed, 3, 1)
+    out_bytes = streams * sq * dv * (2 if out_f16 else 4)
+    got = run(ctx, "ipu_stack_flash_attention_online_f16", out_bytes, [q, k, v],
+              [streams, sq, sk, d, dv, ipus.scale_bits(scale), int(causal), int(out_f16)],
+              np.uint16 if out_f16 else np.float32)
+    if out_f16:
+        got = oracle.f16_to_f32(got)
+    got = got.reshape(streams * sq, dv)
+    want = oracle.attention(oracle.f16_to_f32(q), oracle.f16_to_f32(k), oracle.f16_to_f32(v),
+                            streams, sq, sk, d, dv, causal, scale, row_list=rows)
+    if rows is not None:
+        got = got[np.asarray(rows)]
+    return got, want
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("streams,sq,sk,d", [(2, 256, 256, 128), (3, 300, 300, 128),
+                                             (1, 512, 512, 64), (4, 64, 64, 128),
+                                             (2, 100, 37, 128), (1, 19, 17, 72)])
+def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
+    got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, d, causal)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+def test_attention_scale_and_f16_output(ipus, oracle, ctx):
+    got, want = attention_case(ipus, oracle, ctx, 2, 256, 256, 128, 128, True, scale=0.05,
+                               out_f16=True)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+def test_attention_uniform_values_give_values(ipus, oracle, ctx):
+    """Invariant: V rows all equal -> O = that row for every query (softmax rows sum to 1)."""
+    streams, s, d = 2, 256, 128
+    q = synth(ipus, streams * s * d, 5, 1, 1)
+    k = synth(ipus, streams * s * d, 5, 2, 1)
+    row = synth(ipus, d, 5, 3, 1)
+    v = np.tile(row, streams * s)
+    for causal in (False, True):
+        got = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * d * 4, [q, k, v],
+                  [streams, s, s, d, d, 0, int(causal), 0], np.float32).reshape(-1, d)
+        assert max_rel(got, np.broadcast_to(oracle.f16_to_f32(row), got.shape)) <= 2e-3
+
+
+def test_attention_causal_first_row_is_first_value(ipus, oracle, ctx):
+    """Invariant: under the causal limit (diagnostic.rs:741-745) query 0 sees only key 0."""
+    streams, s, d = 3, 256, 128
+    q = synth(ipus, streams * s * d, 6, 1, 1)
+    k = synth(ipus, streams * s * d, 6, 2, 1)
+    v = synth(ipus, streams * s * d, 6, 3, 1)
+    got = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * d * 4, [q, k, v],
+              [streams, s, s, d, d, 0, 1, 0], np.float32).reshape(streams, s, d)
+    vf = oracle.f16_to_f32(v).reshape(streams, s, d)
+    assert np.allclose(got[:, 0, :], vf[:, 0, :], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("causal,s", [(True, 4096), (False, 2048)])
+def test_attention_baseline_size_sampled_rows(ipus, oracle, ctx, causal, s):
+    """BASELINE config 5 at full size (B8*H16 = 128 streams, D = 128), 256 query
+    rows sampled evenly over all streams (diagnostic.rs:259-267)."""
+    streams, d = 128, 128
+    total = streams * s
+    rows = [i * (total - 1) // 255 for i in range(256)]
+    got, want = attention_case(ipus, oracle, ctx, streams, s, s, d, d, causal, rows=rows, seed=55)
+    assert max_rel(got, want) <= FP16_TOL
+
+
+# ---------------------------------------------------------------------------
+# ABI validation on the device
+# ---------------------------------------------------------------------------
+def test_launch_pointer_arity(ipus, ctx):
+    buf = ctx.alloc(64)
+    with pytest.raises(ipus.KernelAbiError) as e:
+        ctx.launch("ipu_stack_gemm_f16", buf, [buf], [1, 1, 1, 1, 0, 0, 0, 0])
+    assert e.value.status == ipus.ERROR_POINTER_ARITY
+    with pytest.raises(ipus.KernelAbiError) as e:
+        ctx.launch("ipu_stack_no_such_kernel", buf, [], [])
+    assert e.value.status == ipus.ERROR_UNKNOWN_SYMBOL
+    buf.free()

@@ -1,0 +1,229 @@
+"""CPU tests of the ComputeGraph surface and build_package's launch plan.
+
+The randomized shape tests restate crates/ipu-codegen/src/graph.rs:806-966
+(same case construction, own seeds); the error tests follow GraphError
+(graph.rs:221-245)."""
+from __future__ import annotations
+
+import random
+
+import pytest
+
+RANDOM_CASES = 256
+
+
+def dimension(rng):
+    return rng.randint(1, 128)
+
+
+def broadcast_batch(rng):
+    rank = rng.randint(0, 4)
+    left, right, out = [], [], []
+    for _ in range(rank):
+        extent = dimension(rng)
+        kind = rng.randint(0, 2)
+        l, r = (extent, extent) if kind == 0 else ((1, extent) if kind == 1 else (extent, 1))
+        left.append(l)
+        right.append(r)
+        out.append(extent)
+    return left, right, out
+
+
+def test_randomized_batched_gemm_preserves_matrix_axes_and_broadcasts_batch(ipus):
+    rng = random.Random(0x6A656D6D)
+    for case in range(RANDOM_CASES):
+        left, right, expected = broadcast_batch(rng)
+        rows, inner, cols = dimension(rng), dimension(rng), dimension(rng)
+        tl, tr = rng.random() < 0.5, rng.random() < 0.5
+        left += [inner, rows] if tl else [rows, inner]
+        right += [cols, inner] if tr else [inner, cols]
+        expected += [rows, cols]
+        g = ipus.ComputeGraph()
+        l = g.host_input("left", left)
+        r = g.parameter("right", right)
+        out = g.gemm_with_options(l, r, tl, tr)
+        assert g.value_shape(out) == tuple(expected), f"case {case}"
+
+
+def test_randomized_attention_preserves_query_and_value_axes(ipus):
+    rng = random.Random(0x6174746E)
+    for case in range(RANDOM_CASES):
+        qb, kb, expected = broadcast_batch(rng)
+        qr, kr, kc, vc = dimension(rng), dimension(rng), dimension(rng), dimension(rng)
+        g = ipus.ComputeGraph()
+        q = g.host_input("q", qb + [qr, kc])
+        k = g.host_input("k", kb + [kr, kc])
+        v = g.host_input("v", kb + [kr, vc])
+        causal = rng.random() < 0.5
+        scale = None if rng.random() < 0.5 else rng.random() + 0.01
+        out = g.flash_attention_with_options(q, k, v, causal, scale)
+        assert g.value_shape(out) == tuple(expected + [qr, vc]), f"case {case}"
+
+
+def test_randomized_split_heads_preserves_every_projection_element(ipus):
+    rng = random.Random(0x73706C69745F6864)
+    for _ in range(RANDOM_CASES):
+        batch, rows = rng.randint(1, 8), rng.randint(1, 256)
+        heads, width = rng.randint(1, 32), rng.randint(1, 128)
+        g = ipus.ComputeGraph()
+        x = g.host_input("projection", [batch, rows, heads * width])
+        out = g.split_heads(x, heads)
+        assert g.value_shape(out) == (batch * heads, rows, width)
+
+
+def test_randomized_attention_rejects_nonpositive_or_nonfinite_scales(ipus):
+    rng = random.Random(0x7363616C)
+    for case in range(RANDOM_CASES):
+        scale = [0.0, -rng.random() - 1e-6, float("inf"), float("nan")][rng.randint(0, 3)]
+        g = ipus.ComputeGraph()
+        q, k, v = (g.host_input(n, [4, 8]) for n in "qkv")
+        with pytest.raises(ipus.GraphError):
+            g.flash_attention_with_options(q, k, v, rng.random() < 0.5, scale)
+
+
+def test_graph_errors(ipus):
+    g = ipus.ComputeGraph()
+    with pytest.raises(ipus.GraphError, match="graph name must not be empty"):
+        g.host_input("", [1])
+    x = g.host_input("x", [4, 8])
+    with pytest.raises(ipus.GraphError, match="is not available"):
+        g.gelu(12345)
+    with pytest.raises(ipus.GraphError, match="inner dimensions do not match"):
+        g.gemm(x, x)
+    with pytest.raises(ipus.GraphError, match="rank at least two"):
+        g.gemm(g.host_input("v", [8]), x)
+    with pytest.raises(ipus.GraphError, match="cannot be broadcast"):
+        g.add(x, g.host_input("y", [3, 8]))
+    with pytest.raises(ipus.GraphError, match="divisible by heads"):
+        g.split_heads(g.host_input("p", [1, 4, 10]), 3)
+    with pytest.raises(ipus.GraphError, match="nonzero heads"):
+        g.split_heads(x, 2)
+    with pytest.raises(ipus.GraphError, match="head or sequence"):
+        g.flash_attention(x, g.host_input("k", [4, 7]), x)
+
+
+def test_repeat_semantics_and_errors(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("input", [1, 64])
+    weights = [g.parameter(f"layer.{i}.weight", [64, 64]) for i in range(3)]
+    seq = g.value_sequence("layer weights", weights)
+    out = g.repeat(3, [x], [], [seq],
+                   lambda body, a: [body.add(a.carried[0], body.gemm(a.carried[0], a.iterated[0]))])
+    assert g.value_shape(out[0]) == (1, 64)
+    g.set_outputs(out)
+    with pytest.raises(ipus.GraphError, match="repeat count must be nonzero"):
+        g.repeat(0, [x], [], [], lambda b, a: [a.carried[0]])
+    with pytest.raises(ipus.GraphError, match="entries for 4 iterations"):
+        g.repeat(4, [x], [], [seq], lambda b, a: [a.carried[0]])
+    with pytest.raises(ipus.GraphError, match="yielded 0 values for 1 carried"):
+        g.repeat(1, [x], [], [], lambda b, a: [])
+    with pytest.raises(ipus.GraphError, match="does not have the shape"):
+        g.repeat(1, [x], [weights[0]], [], lambda b, a: [a.invariants[0]])
+    with pytest.raises(ipus.GraphError, match="different shape from its first entry"):
+        g.value_sequence("bad", [weights[0], x])
+    # body values do not escape the region
+    captured = []
+
+    def body(b, a):
+        captured.append(b.gelu(a.carried[0]))
+        return [captured[-1]]
+
+    g.repeat(1, [x], [], [], body)
+    with pytest.raises(ipus.GraphError, match="is not available"):
+        g.gelu(captured[0])
+    # a failing body leaves the graph usable
+    with pytest.raises(ipus.GraphError):
+        g.repeat(1, [x], [], [], lambda b, a: [b.gemm(a.carried[0], a.carried[0])])
+    g.gelu(x)
+
+
+def test_build_package_mlp_plan(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("input", [4096, 4096])
+    w1 = g.parameter("w1", [4096, 16384])
+    w2 = g.parameter("w2", [16384, 4096])
+    y = g.gemm(g.gelu(g.gemm(x, w1)), w2)
+    g.set_outputs([y])
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == [
+        "ipu_stack_gemm_f16", "ipu_stack_gelu_tanh_approx_f16", "ipu_stack_gemm_f16"]
+    assert pkg.steps[0][2][:4] == (1, 4096, 16384, 4096)
+    assert [t.name for t in pkg.inputs] == ["input", "w1", "w2"]
+    assert pkg.outputs[0].name == "output.0" and pkg.outputs[0].shape == (4096, 4096)
+    # hidden (128 MiB) and gelu(hidden) (128 MiB) are both live across the GELU
+    assert pkg.arena_bytes == 2 * 4096 * 16384 * 2
+
+
+def test_build_package_arena_reuses_dead_values(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [1024, 1024])
+    v = x
+    for _ in range(6):
+        v = g.gelu(v)
+    g.set_outputs([v])
+    pkg = ipus.build_package(g)
+    # a chain only ever needs two intermediates alive at once
+    assert pkg.arena_bytes == 2 * 1024 * 1024 * 2
+
+
+def test_build_package_precisions_and_casts(ipus):
+    g = ipus.ComputeGraph()
+    q = g.host_input("q", [2, 64, 64])
+    att = g.flash_attention_with_options(q, q, q, causal=True)
+    w = g.parameter("w", [64, 64])
+    out = g.gemm(att, w)
+    g.set_outputs([out, att])
+    pkg = ipus.build_package(g)
+    assert pkg.precision(att) == ipus.PRECISION_F32   # mid.rs:2064-2067
+    assert pkg.precision(out) == ipus.PRECISION_F16
+    symbols = [s[0] for s in pkg.steps]
+    assert symbols[:3] == ["ipu_stack_flash_attention_online_f16", "ipu_stack_cast_f32_f16",
+                           "ipu_stack_gemm_f16"]
+    assert pkg.outputs[1].precision == ipus.PRECISION_F32
+    pkg16 = ipus.build_package(g, ipus.PackageConfig(attention_output_f16=True))
+    assert "ipu_stack_cast_f32_f16" not in [s[0] for s in pkg16.steps]
+
+
+def test_build_package_memory_chain_plan(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [8192, 8192])
+    t = g.transpose(x)
+    bm = g.rearrange(t, ipus.ORDER_BLOCK_MAJOR, 64, 64)
+    r = g.reduce_rows(bm)
+    g.set_outputs([bm, r])
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == [
+        "ipu_stack_transpose_f16", "ipu_stack_rearrange_row_major_f16",
+        "ipu_stack_reduce_rows_f16"]
+    assert pkg.steps[2][2] == (8192, 8192, ipus.ORDER_BLOCK_MAJOR, 64, 64)
+    assert pkg.outputs[0].order == ipus.ORDER_BLOCK_MAJOR
+    assert pkg.outputs[1].shape == (8192,) and pkg.outputs[1].precision == ipus.PRECISION_F32
+
+
+def test_build_package_repeat_unrolls_with_iterated_weights(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("input", [1, 64])
+    ws = [g.parameter(f"w{i}", [64, 64]) for i in range(4)]
+    seq = g.value_sequence("weights", ws)
+    out = g.repeat(4, [x], [], [seq], lambda b, a: [b.gemm(a.carried[0], a.iterated[0])])
+    g.set_outputs(out)
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16"] * 4
+
+
+def test_build_package_output_of_input_is_copied(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [16])
+    g.set_outputs([x, x])
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_copy", "ipu_stack_copy"]
+
+
+def test_build_package_f32_compute(ipus):
+    g = ipus.ComputeGraph()
+    a = g.host_input("a", [4096, 4096])
+    b = g.parameter("b", [4096, 4096])
+    g.set_outputs([g.gemm(a, b)])
+    pkg = ipus.build_package(g, ipus.PackageConfig(compute_precision="f32"))
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f32"]
+    assert pkg.inputs[0].precision == ipus.PRECISION_F32
