@@ -149,6 +149,13 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        L, R are the operand element counts given by the two strides
  *        (trailing-axis numpy broadcasting; the graph executor handles the
  *        general case).
+ *
+ * Roofline calibration (no counterpart in the reference; used by the bench
+ * to report the clock the MFMA pipes sustain for a given operand pattern):
+ *   ipus_calibrate_mfma_f16            out: u64 shader-clock cycles, u64
+ *        100 MHz ticks, then blocks*256 floats; input: operand_count
+ *        fragments of 8 fp16; operand_count, iterations, blocks.  Each
+ *        wave issues 8*iterations v_mfma_f32_32x32x16_f16 on its fragments.
  */
 #define IPUS_MAX_SCALARS 32
 

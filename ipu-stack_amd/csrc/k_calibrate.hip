@@ -1,0 +1,65 @@
+// Roofline calibration: the sustained v_mfma_f32_32x32x16_f16 rate and the
+// shader clock under full MFMA load, for a given operand bit pattern.
+//
+// Each lane loads one A and one B fragment (8 fp16 each) from `operands` and
+// runs `iterations` rounds of 8 independent MFMAs on them; nothing else
+// touches memory until a final store that keeps the results live.  Lane 0 of
+// block 0 records s_memtime (shader clock) and s_memrealtime (100 MHz) around
+// its loop, so clock = d(memtime) / (d(realtime) / 100 MHz).  The MI355X
+// clock under dense MFMA depends on operand entropy (power limit), which is
+// why the calibration takes the operand pattern as input.
+#include "../../include/ipus.h"
+#include "device_common.h"
+#include "kernels.h"
+
+namespace ipus {
+namespace {
+
+__global__ __launch_bounds__(256) void mfma_calibrate_kernel(uint64_t* __restrict__ clocks,
+                                                             float* __restrict__ sink,
+                                                             const half8_t* __restrict__ operands,
+                                                             uint32_t operand_count,
+                                                             uint32_t iterations) {
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const half8_t a = operands[gid % operand_count];
+  const half8_t b = operands[(gid + 7) % operand_count];
+  float16_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) c[j][e] = 0.0f;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  for (uint32_t it = 0; it < iterations; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[j], 0, 0, 0);
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += c[j][e];
+  sink[gid] = s;
+  if (gid == 0) {
+    clocks[0] = t1 - t0;
+    clocks[1] = r1 - r0;
+  }
+}
+
+}  // namespace
+
+uint64_t calibrate_output_bytes(uint32_t blocks) { return 16 + (uint64_t)blocks * 256 * 4; }
+
+int launch_calibrate_mfma_f16(hipStream_t stream, void* out, const void* operands,
+                              uint32_t operand_count, uint32_t iterations, uint32_t blocks) {
+  if (operand_count == 0 || blocks == 0) return IPUS_ERROR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(mfma_calibrate_kernel, dim3(blocks), dim3(256), 0, stream, (uint64_t*)out,
+                     (float*)((uint8_t*)out + 16), (const half8_t*)operands, operand_count,
+                     iterations);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e;
+}
+
+}  // namespace ipus

@@ -5,89 +5,157 @@
 // evaluator's fp32 sgemm followed by one fp16 rounding
 // (crates/ipu-tests/src/diagnostic.rs:533-654, 841-847).
 //
-// Fast kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0):
-//   * block tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each
+// Fast kernel (M % 256 == 0, N % 256 == 0, K % BK == 0):
+//   * block tile 256 x 256 x BK, 256 threads = 4 waves in a 2 x 2 grid, each
 //     wave owns 128 x 128 of C as 4 x 4 tiles of v_mfma_f32_32x32x16_f16;
-//   * both operands are staged in LDS K-contiguous ([row][64 k], 128 B rows)
-//     with the 16-byte chunk index XOR-swizzled by ((r ^ r >> 3) & 7), which
-//     keeps the MFMA fragment reads and both kinds of tile stores free of bank
-//     conflicts;
-//   * an operand whose rows are not K-contiguous in memory (row-major B, or a
-//     transposed A) is loaded as 8 x 8 blocks and transposed in registers
-//     before the LDS store;
-//   * two LDS stages: the next tile's global loads are in flight while the
-//     current tile is multiplied, one barrier per K step;
+//   * operand tiles go global -> LDS with buffer_load ... lds (16 bytes per
+//     lane, no staging registers; out-of-range reads return 0 instead of
+//     faulting).  The DMA writes lane i at base + 16 i, so the LDS swizzle is
+//     produced by choosing which global chunk each lane fetches;
+//   * an operand whose rows are K-contiguous in memory is stored as
+//     [256 rows][BK k] and read with ds_read_b128;
+//   * an operand whose rows are M/N-contiguous (row-major B, transposed A) is
+//     stored as [BK k][256 mn] (512-byte rows) and read with
+//     ds_read_b64_tr_b16: in each 16-lane group, source lane s points at row
+//     k + s/4, column n + 4 (s % 4), and every lane receives 4 consecutive k
+//     of its own column, which is the MFMA fragment layout;
+//   * both swizzles are free of bank conflicts for 32 banks x 4 bytes and for
+//     64 banks x 4 bytes (the XOR patterns below are checked for both);
+//   * kStages LDS stages, each a distinct LDS object: the DMA for K step
+//     kt + kStages - 1 is in flight while step kt is multiplied; fragments are
+//     double-buffered in registers; one raw s_barrier per K step;
 //   * the MFMA computes the tile of C^T (B fragment as the first operand) so
-//     each lane ends up holding 4 consecutive columns of one row of C, stored
-//     as one 8-byte write;
+//     each lane holds 4 consecutive columns of one row of C (one 8-byte store);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
 //     dispatch over 8 XCDs) form a compact group of C tiles sharing L2.
 // General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
+#include <cstdlib>
+
 #include "../../include/ipus.h"
 #include "device_common.h"
 #include "kernels.h"
 
+#define LDS_AS __attribute__((address_space(3)))
+
 namespace ipus {
 namespace {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256;
 constexpr int kThreads = 256;
-constexpr int kTileBytes = kBM * kBK * 2;  // 32 KiB per operand tile
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, dword 3 of the descriptor
+
+typedef short short4_t __attribute__((vector_size(8)));
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
-__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) {
-  return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
+// K-contiguous tile [256 rows][BK k]: byte offset of (row, 16-byte chunk).
+// A b128 fragment read touches 16 consecutive rows of one chunk per 256-byte
+// (64-bank) cycle, 8 per 128-byte (32-bank) cycle; the row-dependent XOR puts
+// them in distinct bank groups under both.
+template <int BK>
+__device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t chunk) {
+  if constexpr (BK == 64) {  // 128-byte rows, 8 chunks
+    return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
+  } else {                   // 64-byte rows, 4 chunks
+    static_assert(BK == 32, "BK is 32 or 64");
+    return row * 64u + ((chunk ^ (((row >> 1) + (row >> 3)) & 3u)) << 4);
+  }
+}
+// MN-contiguous tile [BK k][256 mn]: byte offset of (k, 16-byte chunk along
+// mn).  A transposed read covers rows k..k+3 (k % 4 == 0) and 4 chunks (32
+// lanes); the XOR values {0, 6, 12, 10} give the four rows distinct 64-byte
+// blocks and, within one 16-lane group, distinct 32-byte units.
+__device__ __forceinline__ uint32_t mc_off(uint32_t k, uint32_t chunk) {
+  const uint32_t t = k & 3u;
+  return k * 512u + ((chunk ^ ((t << 1) ^ (t << 2))) << 4);
 }
 
-// Loads this thread's share of a 256-row x 64-k operand tile.
-// KContig: element (r, k) at base[(row0 + r) * ld + k0 + k]
-// else:    element (r, k) at base[(k0 + k) * ld + row0 + r]
-template <bool KContig>
-__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ base, uint64_t ld,
-                                          uint32_t row0, uint32_t k0, u32x4 v[8]) {
-  const uint32_t t = threadIdx.x;
-  if constexpr (KContig) {
-    const uint16_t* p = base + (uint64_t)(row0 + t / 8) * ld + k0 + (t % 8) * 8;
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset,
+                                      uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)lds, 16, voffset, soffset, 0, 0);
+}
+
+template <int BK>
+struct Tile {
+  static constexpr int kBytes = kBM * BK * 2;         // one operand tile
+  static constexpr int kDmaPerWave = kBytes / 1024 / 4;  // 1 KiB per DMA instruction
+};
+
+// Per-lane byte offsets (relative to the block's rsrc base, before the K
+// offset) of the DMA instructions this wave issues for one operand tile.  The
+// DMA writes lane i at base + 16 i, so each lane fetches the global chunk
+// that the swizzle places at its LDS slot.
+template <int BK, bool KContig>
+__device__ __forceinline__ void tile_offsets(uint32_t wave, uint32_t lane, uint32_t ld,
+                                             uint32_t* voff) {
+  constexpr int kChunks = BK / 8;  // 16-byte chunks per K-contiguous row
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = load16(p + (uint64_t)(32 * i) * ld);
-  } else {
-    const uint16_t* p = base + (uint64_t)(k0 + (t / 32) * 8) * ld + row0 + (t % 32) * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = load16(p + (uint64_t)j * ld);
+  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
+    const uint32_t inst = wave * Tile<BK>::kDmaPerWave + j;
+    if constexpr (KContig) {
+      const uint32_t row = inst * (1024 / (BK * 2)) + lane / kChunks;
+      const uint32_t phys = lane % kChunks;
+      // invert the XOR of kc_off for this row
+      const uint32_t chunk = (kc_off<BK>(row, phys) - row * (BK * 2)) >> 4;
+      voff[j] = (row * ld + chunk * 8) * 2;
+    } else {
+      const uint32_t k = inst * 2 + lane / 32;  // 2 rows of 512 bytes
+      const uint32_t phys = lane % 32;
+      const uint32_t chunk = (mc_off(k, phys) - k * 512u) >> 4;
+      voff[j] = (k * ld + chunk * 8) * 2;
+    }
   }
 }
 
-template <bool KContig>
-__device__ __forceinline__ void store_tile(uint8_t* lds, const u32x4 v[8]) {
-  const uint32_t t = threadIdx.x;
+template <int BK>
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
+                                           uint32_t wave, const uint32_t* voff, uint32_t soffset) {
+#pragma unroll
+  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j)
+    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024, voff[j], soffset);
+}
+
+// Fragment for v_mfma_f32_32x32x16_f16: lane holds X[row0 + lane % 32][16 ks +
+// 8 (lane / 32) .. +7] of the operand whose rows are `row0 ..` (m for A, n for B).
+template <int BK, bool KContig>
+__device__ __forceinline__ half8_t read_frag(const uint8_t* tile, uint32_t row0, uint32_t ks,
+                                             uint32_t lane) {
   if constexpr (KContig) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t r = t / 8 + 32 * i;
-      *reinterpret_cast<u32x4*>(lds + swz(r, t % 8)) = v[i];
-    }
+    return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(
+                                           tile + kc_off<BK>(row0 + lane % 32, ks * 2 + lane / 32)));
   } else {
-    u32x4 w[8];
-    transpose8x8_u16(v, w);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t r = (t % 32) * 8 + i;
-      *reinterpret_cast<u32x4*>(lds + swz(r, t / 32)) = w[i];
-    }
+    const uint32_t group = lane / 16, s = lane % 16;
+    const uint32_t mn = row0 + (group % 2) * 16 + 4 * (s % 4);
+    const uint32_t k = ks * 16 + (group / 2) * 8 + s / 4;
+    const uint32_t byte_in_chunk = (mn % 8) * 2;
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (LDS_AS short4_t*)(tile + mc_off(k, mn / 8) + byte_in_chunk));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (LDS_AS short4_t*)(tile + mc_off(k + 4, mn / 8) + byte_in_chunk));
+    return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 }
 
-__device__ __forceinline__ half8_t read_frag(const uint8_t* lds, uint32_t row, uint32_t chunk) {
-  return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(lds + swz(row, chunk)));
-}
-
-template <bool TransposeLeft, bool TransposeRight>
+template <bool TransposeLeft, bool TransposeRight, int BK, int kStages>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
     uint64_t left_batch_stride, uint64_t right_batch_stride) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  static_assert(kStages == 2 || kStages == 4, "2 or 4 stages");
+  static_assert(kStages * 2 * Tile<BK>::kBytes <= 160 * 1024, "LDS budget");
+  constexpr int kTileBytes = Tile<BK>::kBytes;
+  constexpr int kDma = Tile<BK>::kDmaPerWave;
+  // Stages are distinct LDS objects (unused ones are not allocated).
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a2[kStages == 4 ? kTileBytes : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b2[kStages == 4 ? kTileBytes : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a3[kStages == 4 ? kTileBytes : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b3[kStages == 4 ? kTileBytes : 16];
+  constexpr bool kAK = !TransposeLeft;  // A rows (m) K-contiguous
+  constexpr bool kBK_ = TransposeRight; // B^T rows (n) K-contiguous
 
   const uint32_t nbm = M / kBM, nbn = N / kBN;
   const uint32_t tiles = nbm * nbn;
@@ -100,19 +168,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   const uint32_t in_group = pid % (kGroup * nbn);
   const uint32_t bm = first_m + in_group % group_rows;
   const uint32_t bn = in_group / group_rows;
+  const uint32_t m0 = bm * kBM, n0 = bn * kBN;
 
   const uint64_t batch = blockIdx.y;
   const uint16_t* A = left + batch * left_batch_stride;
   const uint16_t* B = right + batch * right_batch_stride;
   uint16_t* C = out + batch * (uint64_t)M * N;
-  // Leading dimensions of the stored operands.
-  const uint64_t lda = TransposeLeft ? M : K;
-  const uint64_t ldb = TransposeRight ? K : N;
-  constexpr bool kAContig = !TransposeLeft;  // A rows (m) K-contiguous
-  constexpr bool kBContig = TransposeRight;  // B^T rows (n) K-contiguous
 
-  const uint32_t m0 = bm * kBM, n0 = bn * kBN;
+  // Buffer descriptors based at this block's first row / column.
+  const uint16_t* a_base = kAK ? A + (uint64_t)m0 * K : A + m0;
+  const uint16_t* b_base = kBK_ ? B + (uint64_t)n0 * K : B + n0;
+  const uint64_t a_bytes = (uint64_t)M * K * 2 - (uint64_t)(a_base - A) * 2;
+  const uint64_t b_bytes = (uint64_t)N * K * 2 - (uint64_t)(b_base - B) * 2;
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a_base, 0, (int)(a_bytes > 0x7fffffffull ? 0x7fffffff : a_bytes), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)b_base, 0, (int)(b_bytes > 0x7fffffffull ? 0x7fffffff : b_bytes), kBufferFlags);
+
   const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  uint32_t a_voff[kDma], b_voff[kDma];
+  tile_offsets<BK, kAK>(wave, lane, kAK ? K : M, a_voff);
+  tile_offsets<BK, kBK_>(wave, lane, kBK_ ? K : N, b_voff);
+  // K advance per step in bytes.
+  const uint32_t a_kstep = kAK ? BK * 2 : BK * M * 2;
+  const uint32_t b_kstep = kBK_ ? BK * 2 : BK * N * 2;
+
   const uint32_t wm = (wave / 2) * 128, wn = (wave % 2) * 128;
 
   float16_t acc[4][4];
@@ -123,43 +203,98 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  u32x4 ra[8], rb[8];
-  load_tile<kAContig>(A, lda, m0, 0, ra);
-  load_tile<kBContig>(B, ldb, n0, 0, rb);
-  store_tile<kAContig>((smem + 0 + (0) * 2 * kTileBytes), ra);
-  store_tile<kBContig>((smem + kTileBytes + (0) * 2 * kTileBytes), rb);
-  __syncthreads();
+  const uint32_t ksteps = K / BK;
+  auto clamp = [&](uint32_t k) { return k < ksteps ? k : ksteps - 1; };
+  auto fetch = [&](uint8_t* ta, uint8_t* tb, uint32_t k) {
+    issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
+    issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
+  };
+  // Prologue: K steps 0 .. kStages-2 (clamped: a short K re-fetches its last
+  // step into stages that are never read).
+  fetch(lds_a0, lds_b0, 0);
+  if constexpr (kStages == 4) {
+    fetch(lds_a1, lds_b1, clamp(1));
+    fetch(lds_a2, lds_b2, clamp(2));
+  }
 
-  const uint32_t ksteps = K / kBK;
-  for (uint32_t kt = 0; kt < ksteps; ++kt) {
-    const uint32_t cur = kt & 1;
-    const bool more = kt + 1 < ksteps;
-    if (more) {
-      load_tile<kAContig>(A, lda, m0, (kt + 1) * kBK, ra);
-      load_tile<kBContig>(B, ldb, n0, (kt + 1) * kBK, rb);
+  // One K step: multiply stage kt % kStages while K step kt + kStages - 1 is
+  // fetched into the stage freed by step kt - 1.  Distinct LDS objects and
+  // the unrolled loop let the compiler see that the DMA target never aliases
+  // the fragment reads.
+  auto step = [&](const uint8_t* ta, const uint8_t* tb, uint8_t* na, uint8_t* nb, uint32_t kt) {
+    // A raw s_barrier: __syncthreads() would add a workgroup fence, which
+    // drains every outstanding DMA (vmcnt(0)) and defeats the prefetch.
+    // The vmcnt wait leaves the younger stages' DMA in flight; lgkmcnt(0)
+    // retires this wave's fragment reads of step kt - 1 before any wave may
+    // overwrite that stage; the asm is also a compiler barrier for the LDS
+    // accesses around it.
+    if constexpr (kStages == 4) {
+      static_assert(kStages != 4 || 2 * 2 * kDma == 16, "vmcnt immediate below");
+      asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    const uint8_t* la = (smem + 0 + (cur) * 2 * kTileBytes);
-    const uint8_t* lb = (smem + kTileBytes + (cur) * 2 * kTileBytes);
+    // The last steps re-fetch step ksteps - 1 into stages that are never
+    // read, keeping the body one branch-free scheduling region; the
+    // outstanding DMA is drained after the loop.
+    fetch(na, nb, clamp(kt + kStages - 1));
+    half8_t fa[2][4], fb[2][4];
 #pragma unroll
-    for (uint32_t ks = 0; ks < kBK / 16; ++ks) {
-      const uint32_t chunk = ks * 2 + lane / 32;
-      half8_t fa[4], fb[4];
+    for (int i = 0; i < 4; ++i) fa[0][i] = read_frag<BK, kAK>(ta, wm + 32 * i, 0, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = read_frag(la, wm + i * 32 + lane % 32, chunk);
+    for (int j = 0; j < 4; ++j) fb[0][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, 0, lane);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) fb[j] = read_frag(lb, wn + j * 32 + lane % 32, chunk);
+    for (uint32_t ks = 0; ks < BK / 16; ++ks) {
+      const uint32_t cur = ks & 1;
+      if (ks + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[cur ^ 1][i] = read_frag<BK, kAK>(ta, wm + 32 * i, ks + 1, lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[cur ^ 1][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, ks + 1, lane);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
     }
-    if (more) {
-      store_tile<kAContig>((smem + 0 + (cur ^ 1) * 2 * kTileBytes), ra);
-      store_tile<kBContig>((smem + kTileBytes + (cur ^ 1) * 2 * kTileBytes), rb);
+    // Issue order: the first substep's fragment reads, then each MFMA
+    // followed by one fragment read of the next substep (and, during the
+    // first substep, one prefetch DMA), so LDS and memory latency hide under
+    // the matrix pipe.
+    constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
+    constexpr int kSubs = BK / 16;
+    __builtin_amdgcn_sched_group_barrier(0x100, kDsPerSub, 0);
+#pragma unroll
+    for (int sub = 0; sub < kSubs; ++sub) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (sub == 0 && m < 2 * kDma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (sub + 1 < kSubs && m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
-    __syncthreads();
+  };
+
+  uint32_t kt = 0;
+  if constexpr (kStages == 4) {
+    for (; kt + 3 < ksteps; kt += 4) {
+      step(lds_a0, lds_b0, lds_a3, lds_b3, kt);
+      step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
+      step(lds_a2, lds_b2, lds_a1, lds_b1, kt + 2);
+      step(lds_a3, lds_b3, lds_a2, lds_b2, kt + 3);
+    }
+    if (kt < ksteps) step(lds_a0, lds_b0, lds_a3, lds_b3, kt);
+    if (kt + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
+    if (kt + 2 < ksteps) step(lds_a2, lds_b2, lds_a1, lds_b1, kt + 2);
+  } else {
+    for (; kt + 1 < ksteps; kt += 2) {
+      step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
+      step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
+    }
+    if (kt < ksteps) step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the redundant prefetches
 
   // acc[i][j][r] = C[m0 + wm + 32 i + lane % 32][n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4]
   const uint32_t row = m0 + wm + lane % 32;
@@ -223,21 +358,31 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
   }
 }
 
-template <bool TL, bool TR>
+template <bool TL, bool TR, int BK, int S>
 int launch_fast(hipStream_t stream, const GemmArgs& a) {
   const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
-  constexpr size_t lds = 4 * kTileBytes;  // two stages of A and B
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_f16_256_kernel<TL, TR>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_status(e);
-    configured = true;
-  }
-  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR>), dim3(tiles, a.batches), dim3(kThreads), lds,
-                     stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
-                     a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, BK, S>), dim3(tiles, a.batches), dim3(kThreads),
+                     0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
+                     (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
+                     a.right_batch_stride);
   return hip_status(hipGetLastError());
+}
+
+template <int BK, int S>
+int dispatch_fast(hipStream_t stream, const GemmArgs& a) {
+  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false, BK, S>(stream, a);
+  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true, BK, S>(stream, a);
+  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false, BK, S>(stream, a);
+  return launch_fast<true, true, BK, S>(stream, a);
+}
+
+// Pipeline variant: 0 = BK 64 x 2 stages, 1 = BK 32 x 4 stages.
+int pipeline_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("IPUS_GEMM_F16_PIPELINE");
+    return e ? std::atoi(e) : 0;
+  }();
+  return v;
 }
 
 }  // namespace
@@ -248,11 +393,15 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   const bool aligned = ((uintptr_t)a.left % 16 == 0) && ((uintptr_t)a.right % 16 == 0) &&
                        ((uintptr_t)a.out % 16 == 0) && a.left_batch_stride % 8 == 0 &&
                        a.right_batch_stride % 8 == 0;
-  if (aligned && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner % kBK == 0 && a.inner > 0) {
-    if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
-    if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
-    if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);
-    return launch_fast<true, true>(stream, a);
+  // Buffer offsets are 32-bit: per-block offsets stay below 2^31 bytes.
+  const uint64_t a_span = a.transpose_left ? (uint64_t)a.inner * a.rows * 2 : 256ull * a.inner * 2;
+  const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
+  const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
+  if (aligned && fits && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner > 0) {
+    const int v = pipeline_variant();
+    if (v == 1 && a.inner % 32 == 0) return dispatch_fast<32, 4>(stream, a);
+    if (a.inner % 64 == 0) return dispatch_fast<64, 2>(stream, a);
+    if (a.inner % 32 == 0) return dispatch_fast<32, 4>(stream, a);
   }
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,

@@ -78,6 +78,12 @@ int launch_add(hipStream_t stream, const AddArgs& a);
 // element_bytes 2 or 4.
 int launch_split_heads(hipStream_t stream, void* dst, const void* src, uint32_t batch,
                        uint32_t rows, uint32_t heads, uint32_t channels, uint32_t element_bytes);
+// Roofline calibration (k_calibrate.hip): `out` receives two u64 (shader
+// clock cycles, 100 MHz ticks of lane 0 of block 0) and a float sink of
+// blocks * 256 values; `operands` holds operand_count fragments of 8 fp16.
+uint64_t calibrate_output_bytes(uint32_t blocks);
+int launch_calibrate_mfma_f16(hipStream_t stream, void* out, const void* operands,
+                              uint32_t operand_count, uint32_t iterations, uint32_t blocks);
 // Stored order (AmpLeft, AmpTransposedRight, BlockMajor) -> row-major.
 int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
                             uint32_t row_block, uint32_t column_block, uint32_t matrices,

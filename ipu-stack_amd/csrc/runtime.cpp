@@ -424,6 +424,12 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_gelu_f16(c->stream, o, i[0], s[0]);
        }},
+      // Roofline calibration (no reference counterpart): sustained MFMA rate
+      // and shader clock for the given operand pattern.
+      {"ipus_calibrate_mfma_f16", 1, {"operand_count", "iterations", "blocks"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_calibrate_mfma_f16(c->stream, o, i[0], s[0], s[1], s[2]);
+       }},
       {"ipu_stack_copy", 1, {"byte_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          if (s[0] == 0) return 0;
