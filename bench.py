@@ -197,6 +197,26 @@ def cpu_baseline(ipus, n=8192, min_seconds=10.0):
     }
 
 
+def traffic_probe(ipus, ctx, n=8192, copy_bytes=256 << 20):
+    """Untimed launches for the rocprofv3 --pmc passes that give
+    roofline.traffic: the headline GEMM, then a plain 16-byte-vector copy of
+    `copy_bytes` whose FETCH_SIZE / WRITE_SIZE calibrate the counters' unit."""
+    a = ctx.upload(ipus.synth_f16(n * n, 2024, 1, ipus.UNIFORM))
+    b = ctx.upload(ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM))
+    c = ctx.alloc(n * n * 2)
+    for _ in range(3):
+        ctx.launch("ipu_stack_gemm_f16", c, [a, b], gemm_scalars(n))
+    ctx.sync()
+    src, dst = ctx.alloc(copy_bytes), ctx.alloc(copy_bytes)
+    ctx.memset(src, 1)
+    for _ in range(3):
+        ctx.launch("ipu_stack_copy", dst, [src], [copy_bytes])
+    ctx.sync()
+    for x in (a, b, c, src, dst):
+        x.free()
+    log(f"traffic probe: 3x gemm_f16 {n}^3, 3x copy {copy_bytes} B")
+
+
 def committed_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE runs (profiles/gemm_f16_8192_traffic.json)."""
@@ -214,6 +234,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the headline GEMM and a calibration copy (for --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -227,6 +249,11 @@ def main() -> int:
     info = ctx.device_info()
     log(f"device: {info['name']} {info['arch']} CUs={info['compute_units']} "
         f"clock={info['clock_khz'] / 1e3:.0f} MHz")
+
+    if args.traffic_probe:
+        traffic_probe(ipus, ctx)
+        ctx.close()
+        return 0
 
     n = 8192
     flops = 2.0 * n ** 3

@@ -350,6 +350,17 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(uint8_t* __restrict
   if (tail < bytes && tail < vectors * 16 + 16) dst[tail] = 0;
 }
 
+// Plain device copy: 16-byte vectors (both pointers 16-byte aligned), then
+// the byte tail; `vectors` = 0 copies byte by byte.
+__global__ __launch_bounds__(kThreads) void copy_bytes_kernel(uint8_t* __restrict__ dst,
+                                                              const uint8_t* __restrict__ src,
+                                                              uint64_t vectors, uint64_t bytes) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t first = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (uint64_t v = first; v < vectors; v += stride) store16(dst + v * 16, load16(src + v * 16));
+  for (uint64_t b = vectors * 16 + first; b < bytes; b += stride) dst[b] = src[b];
+}
+
 __global__ __launch_bounds__(kThreads) void cast_f32_f16_kernel(uint16_t* __restrict__ dst,
                                                                 const float* __restrict__ src,
                                                                 uint64_t count) {
@@ -592,6 +603,14 @@ int launch_gelu_f16(hipStream_t stream, void* dst, const void* src, uint64_t cou
   else
     hipLaunchKernelGGL(gelu_f16_scalar_kernel, dim3(grid_for(count)), dim3(kThreads), 0, stream,
                        (uint16_t*)dst, (const uint16_t*)src, count);
+  return hip_status(hipGetLastError());
+}
+
+int launch_copy(hipStream_t stream, void* dst, const void* src, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  const uint64_t vectors = aligned16(dst) && aligned16(src) ? bytes / 16 : 0;
+  hipLaunchKernelGGL(copy_bytes_kernel, dim3(grid_for(vectors ? vectors : bytes)), dim3(kThreads),
+                     0, stream, (uint8_t*)dst, (const uint8_t*)src, vectors, bytes);
   return hip_status(hipGetLastError());
 }
 

@@ -59,6 +59,7 @@ int launch_reduce_sum_f16(hipStream_t stream, void* dst, const void* initial, co
                           uint32_t remote_partials, uint32_t count);
 int launch_gelu_f16(hipStream_t stream, void* dst, const void* src, uint64_t count);
 int launch_fill_zero(hipStream_t stream, void* dst, uint64_t bytes);
+int launch_copy(hipStream_t stream, void* dst, const void* src, uint64_t bytes);
 int launch_cast_f32_to_f16(hipStream_t stream, void* dst, const void* src, uint64_t count);
 int launch_cast_f16_to_f32(hipStream_t stream, void* dst, const void* src, uint64_t count);
 // out = left + right with numpy broadcasting over up to 6 axes; strides are

@@ -432,9 +432,7 @@ const std::vector<KernelEntry>& registry() {
        }},
       {"ipu_stack_copy", 1, {"byte_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         if (s[0] == 0) return 0;
-         const hipError_t e = hipMemcpyAsync(o, i[0], s[0], hipMemcpyDeviceToDevice, c->stream);
-         return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e;
+         return launch_copy(c->stream, o, i[0], s[0]);
        }},
   };
   return entries;

@@ -31,6 +31,26 @@ def run(ctx, symbol, out_nbytes, inputs, scalars, dtype=np.uint16):
 
 
 # ---------------------------------------------------------------------------
+# Plain copy (output copies of packages; the traffic calibration kernel)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("nbytes,src_off,dst_off", [
+    (1, 0, 0), (15, 0, 0), (16, 0, 0), (1000, 0, 0), (4099, 3, 5), (4096, 16, 32),
+    (1 << 26, 0, 0)])
+def test_copy_bytes(ipus, ctx, nbytes, src_off, dst_off):
+    rng = np.random.default_rng(nbytes)
+    data = rng.integers(0, 256, nbytes + 64, dtype=np.uint8)
+    src = ctx.upload(data)
+    dst = ctx.upload(np.full(nbytes + 64, 0xA5, dtype=np.uint8))
+    ctx.launch("ipu_stack_copy", dst.ptr + dst_off, [src.ptr + src_off], [nbytes])
+    got = dst.download(np.uint8)
+    want = np.full(nbytes + 64, 0xA5, dtype=np.uint8)
+    want[dst_off:dst_off + nbytes] = data[src_off:src_off + nbytes]
+    assert np.array_equal(got, want)
+    src.free()
+    dst.free()
+
+
+# ---------------------------------------------------------------------------
 # Transpose and rearranges (bit-exact)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("matrices,rows,cols", [
