@@ -8,292 +8,308 @@
 // causal, 741-745; scale default 1/sqrt(width), 733-736).
 //
 // Fast kernel (width == value width in {64, 128}):
-//   * 256 threads = 4 waves; a wave owns 64 queries (two 32-query tiles), a
-//     block 256 queries of one stream; keys stream through LDS in blocks of 64
-//     with two stages (next block's loads in flight during the math);
+//   * 256 threads = 4 waves; a wave owns 32 queries, a workgroup 128 queries
+//     of one stream; two workgroups share a CU (launch bound), so one SIMD
+//     runs the softmax of one wave while the MFMA pipe serves the other;
+//   * keys stream through LDS in blocks of 64 with two stages.  K and V tiles
+//     are copied global -> LDS with buffer_load ... lds (16 bytes per lane, no
+//     staging registers; rows past the end of the stream read as 0), both
+//     stored row-major [64 keys][D] with an XOR swizzle of 16-byte chunks;
 //   * scores are computed transposed, S^T = K Q^T, with
-//     v_mfma_f32_32x32x16_f16 (K rows from LDS as the first operand, Q
-//     fragments resident in registers as the second), so each lane holds 16
-//     keys of ONE query: the row max needs one cross-lane exchange (lane ^ 32)
+//     v_mfma_f32_32x32x16_f16 (K fragments by ds_read_b128 as the first
+//     operand, Q fragments resident in registers as the second), so a lane
+//     holds 32 keys of ONE query: the row max needs one exchange (lane ^ 32)
 //     and the running sum none until the end;
-//   * the output is accumulated transposed too, O^T += V^T P^T: the fp16
+//   * the output is accumulated transposed, O^T += V^T P^T: the fp16
 //     probabilities are the second MFMA operand straight from the score
-//     registers (no shuffle), because V^T is stored in LDS with its keys
-//     permuted to match the score accumulator layout; the rescale by
-//     exp(m_old - m_new) is lane-local;
-//   * causal: key blocks past the block's last query are never loaded, a wave
-//     skips blocks past its own last query, and blocks are issued heaviest
-//     first.
+//     registers, and the matching V^T fragments come from the row-major V
+//     tile through ds_read_b64_tr_b16, whose 4-key runs are chosen to follow
+//     the score accumulator's key order;
+//   * the running max moves only when a block's max exceeds it by more than
+//     kRescaleSlack (log2 units): the result is exact for any reference
+//     point, probabilities stay <= 2^kRescaleSlack, and most blocks skip the
+//     rescale of the output accumulators;
+//   * causal: key blocks past the workgroup's last query are never loaded, a
+//     wave skips blocks past its own last query.
+//   * workgroups are remapped so each XCD (round-robin dispatch over 8) runs
+//     whole streams, heaviest query blocks first, sharing K and V in its L2.
 #include "../../include/ipus.h"
 #include "device_common.h"
 #include "kernels.h"
+
+#define LDS_AS __attribute__((address_space(3)))
 
 namespace ipus {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kQueriesPerBlock = 256;
+constexpr int kQueriesPerWave = 32;
+constexpr int kQueriesPerBlock = 128;
 constexpr int kKeysPerBlock = 64;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.0f;
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, dword 3 of the descriptor
+
+typedef short short4_t __attribute__((vector_size(8)));
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
-// K tile: [64 keys][D] fp16, rows of D*2 bytes, 16-byte chunks XOR (key & 7).
+// Tiles of 64 keys x D fp16, rows of D * 2 bytes, 16-byte chunks swizzled by
+// row.  K is read with ds_read_b128 (16 consecutive rows, one chunk, per
+// 256-byte cycle); V with ds_read_b64_tr_b16 (4 consecutive rows x 4 chunks
+// per 32 lanes).  The XORs give each of those reads distinct banks.
 template <int D>
-__device__ __forceinline__ uint32_t k_off(uint32_t key, uint32_t chunk) {
-  return key * (D * 2) + ((chunk ^ (key & 7u)) << 4);
-}
-// V^T tile: [D][64 key slots] fp16, 128-byte rows, chunks XOR ((d ^ d>>3) & 7).
-__device__ __forceinline__ uint32_t vt_off(uint32_t d, uint32_t chunk) {
-  return d * 128u + ((chunk ^ ((d ^ (d >> 3)) & 7u)) << 4);
-}
-
-// Key slot inside a 32-key group: key = 8a + 4g + b is stored at slot
-// (a/2)*16 + g*8 + (a%2)*4 + b, so that PV MFMA h of the group reads, in lane
-// group g, the 8 keys {8(2h)+4g+b, 8(2h+1)+4g+b} that score accumulator
-// elements 8h..8h+7 of that lane hold.
-
-template <int D>
-struct Tiles {
-  static constexpr uint32_t kBytes = kKeysPerBlock * D * 2;  // per operand
+struct KvTile {
+  static constexpr uint32_t kRowBytes = D * 2;
+  static constexpr uint32_t kChunks = D / 8;
+  static constexpr uint32_t kBytes = kKeysPerBlock * D * 2;
+  static constexpr uint32_t kDma = kBytes / 16 / kThreads;  // DMA instructions per thread
 };
-
-// Threads 128..255 load K (D/8 * 64 / 128 vectors each), threads 0..127 load
-// V as 8x8 blocks (one block per thread for D = 128, half for D = 64).
 template <int D>
-struct KvRegs {
-  u32x4 v[8];
-};
-
+__device__ __forceinline__ uint32_t k_swz(uint32_t row) {
+  return D == 128 ? (row & 15u) : ((row >> 1) & 7u);
+}
 template <int D>
-__device__ __forceinline__ void load_kv(const uint16_t* __restrict__ K,
-                                        const uint16_t* __restrict__ V, uint32_t key0,
-                                        uint32_t key_rows, KvRegs<D>& r) {
-  const uint32_t t = threadIdx.x;
-  constexpr uint32_t chunks = D / 8;  // 16-byte chunks per row
-  if (t >= 128) {
-    const uint32_t u = t - 128;
-    // 64 rows x chunks vectors over 128 threads.
-    constexpr uint32_t per = 64 * chunks / 128;
+__device__ __forceinline__ uint32_t v_swz(uint32_t row) {
+  return D == 128 ? ((row & 3u) << 2) : (((row >> 1) & 1u) << 2);
+}
+template <int D>
+__device__ __forceinline__ uint32_t k_off(uint32_t row, uint32_t chunk) {
+  return row * KvTile<D>::kRowBytes + ((chunk ^ k_swz<D>(row)) << 4);
+}
+template <int D>
+__device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
+  return row * KvTile<D>::kRowBytes + ((chunk ^ v_swz<D>(row)) << 4);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// Byte offsets within a key block of the chunks this thread's DMA
+// instructions fetch: instruction i of thread t fills LDS slot i * 256 + t,
+// so it loads the chunk that the swizzle places there.
+template <int D, bool IsK>
+__device__ __forceinline__ void kv_offsets(uint32_t* voff) {
 #pragma unroll
-    for (uint32_t i = 0; i < per; ++i) {
-      const uint32_t idx = u + 128 * i;
-      uint32_t key = key0 + idx / chunks;
-      key = key < key_rows ? key : key_rows - 1;
-      r.v[i] = load16(K + (uint64_t)key * D + (idx % chunks) * 8);
-    }
-  } else {
-    // 8x8 blocks: key group kg (8 groups), d chunk dc (chunks).  D=128: 128
-    // blocks, one per thread; D=64: 64 blocks on threads 0..63.
-    if (t < 8 * chunks) {
-      const uint32_t dc = t % chunks, kg = t / chunks;
-#pragma unroll
-      for (uint32_t j = 0; j < 8; ++j) {
-        uint32_t key = key0 + kg * 8 + j;
-        key = key < key_rows ? key : key_rows - 1;
-        r.v[j] = load16(V + (uint64_t)key * D + dc * 8);
-      }
-    }
+  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) {
+    const uint32_t slot = i * kThreads + threadIdx.x;
+    const uint32_t row = slot / KvTile<D>::kChunks, phys = slot % KvTile<D>::kChunks;
+    const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
+    voff[i] = row * KvTile<D>::kRowBytes + chunk * 16;
   }
 }
 
 template <int D>
-__device__ __forceinline__ void store_kv(uint8_t* lds_k, uint8_t* lds_vt, const KvRegs<D>& r) {
-  const uint32_t t = threadIdx.x;
-  constexpr uint32_t chunks = D / 8;
-  if (t >= 128) {
-    const uint32_t u = t - 128;
-    constexpr uint32_t per = 64 * chunks / 128;
+__device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t k_rsrc,
+                                         __amdgpu_buffer_rsrc_t v_rsrc, uint8_t* lk, uint8_t* lv,
+                                         const uint32_t* k_voff, const uint32_t* v_voff,
+                                         uint32_t block_bytes) {
+  const uint32_t wave = threadIdx.x / kWave;
 #pragma unroll
-    for (uint32_t i = 0; i < per; ++i) {
-      const uint32_t idx = u + 128 * i;
-      *reinterpret_cast<u32x4*>(lds_k + k_off<D>(idx / chunks, idx % chunks)) = r.v[i];
-    }
-  } else if (t < 8 * chunks) {
-    const uint32_t dc = t % chunks, kg = t / chunks;
-    u32x4 w[8];
-    transpose8x8_u16(r.v, w);
-    // w[i] = keys kg*8 .. kg*8+7 of d = dc*8 + i.
-    const uint32_t group32 = kg / 4;  // which 32-key group
-    const uint32_t a = kg % 4;        // keys 8a .. 8a+7 of the group
-    const uint32_t h = a / 2, half = a % 2;
+  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
+    dma16(k_rsrc, lk + (i * kThreads + wave * kWave) * 16, k_voff[i] + block_bytes);
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-      const uint32_t d = dc * 8 + i;
-      // keys 8a+0..3 -> g = 0, keys 8a+4..7 -> g = 1; each a 4-slot run at
-      // byte offset half*8 inside chunk group32*4 + h*2 + g.
-      uint8_t* base0 = lds_vt + vt_off(d, group32 * 4 + h * 2 + 0) + half * 8;
-      uint8_t* base1 = lds_vt + vt_off(d, group32 * 4 + h * 2 + 1) + half * 8;
-      *reinterpret_cast<u32x2*>(base0) = u32x2{w[i][0], w[i][1]};
-      *reinterpret_cast<u32x2*>(base1) = u32x2{w[i][2], w[i][3]};
-    }
-  }
+  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
+    dma16(v_rsrc, lv + (i * kThreads + wave * kWave) * 16, v_voff[i] + block_bytes);
+}
+
+// K fragment (first operand of S^T = K Q^T): lane holds
+// K[32 st + lane % 32][16 ks + 8 (lane / 32) .. +7].
+template <int D>
+__device__ __forceinline__ half8_t k_frag(const uint8_t* lk, uint32_t st, uint32_t ks,
+                                          uint32_t lane) {
+  return __builtin_bit_cast(
+      half8_t, *reinterpret_cast<const u32x4*>(lk + k_off<D>(st * 32 + lane % 32, ks * 2 + lane / 32)));
+}
+
+// V^T fragment (first operand of O^T += V^T P^T) for d tile dt and the 16
+// keys 32 st + 16 h + {0..15}: lane holds d = 32 dt + lane % 32 and, in
+// element e, key 32 st + 16 h + 8 (e / 4) + 4 (lane / 32) + e % 4, the key
+// order of score accumulator elements 8 h .. 8 h + 7.  Each transposed read
+// returns 4 consecutive keys: in a 16-lane group, source lane s addresses row
+// key0 + s / 4, columns d0 + 4 (s % 4) .. +3.
+template <int D>
+__device__ __forceinline__ half8_t v_frag(const uint8_t* lv, uint32_t st, uint32_t h, uint32_t dt,
+                                          uint32_t lane) {
+  const uint32_t s = lane % 16, g = lane / 32, dg = (lane / 16) % 2;
+  const uint32_t key = 32 * st + 16 * h + 4 * g + s / 4;
+  const uint32_t d = 32 * dt + 16 * dg + 4 * (s % 4);
+  const uint32_t byte = (d % 8) * 2;
+  const short4_t lo =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(lv + v_off<D>(key, d / 8) + byte));
+  const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (LDS_AS short4_t*)(lv + v_off<D>(key + 8, d / 8) + byte));
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 template <int D, bool Causal, bool OutF16>
-__global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
     float scale_log2) {
   constexpr uint32_t kDT = D / 32;  // output d tiles
   constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
-  constexpr uint32_t kBytes = Tiles<D>::kBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kBytes];
+  constexpr uint32_t kTile = KvTile<D>::kBytes;
+  // Two stages, each a distinct LDS object so the compiler can see that the
+  // DMA into one stage never aliases the fragment reads of the other.
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTile];
 
   const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const uint32_t stream = blockIdx.x % streams;
-  const uint32_t qb = Causal ? qblocks - 1 - blockIdx.x / streams : blockIdx.x / streams;
+  const uint32_t total = qblocks * streams;
+  uint32_t pid = blockIdx.x;
+  if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;  // XCD-contiguous
+  const uint32_t stream = pid / qblocks;
+  const uint32_t qb = Causal ? qblocks - 1 - pid % qblocks : pid % qblocks;
   const uint32_t q0 = qb * kQueriesPerBlock;
   const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t wq0 = q0 + wave * 64;  // first query of this wave
+  const uint32_t wq0 = q0 + wave * kQueriesPerWave;  // first query of this wave
 
   const uint16_t* Q = query + (uint64_t)stream * query_rows * D;
   const uint16_t* K = key + (uint64_t)stream * key_rows * D;
   const uint16_t* V = value + (uint64_t)stream * key_rows * D;
-
-  // Q fragments (second MFMA operand): lane holds Q[q][16 ks + 8 (lane/32) ..+7].
-  half8_t qf[2][kKS];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    uint32_t q = wq0 + qt * 32 + lane % 32;
-    q = q < query_rows ? q : query_rows - 1;
-#pragma unroll
-    for (uint32_t ks = 0; ks < kKS; ++ks)
-      qf[qt][ks] = __builtin_bit_cast(half8_t, load16(Q + (uint64_t)q * D + ks * 16 + (lane / 32) * 8));
-  }
-
-  float16_t o[2][kDT];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (uint32_t dt = 0; dt < kDT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[qt][dt][e] = 0.0f;
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.0f, 0.0f};
+  const int stream_bytes = (int)(key_rows * (uint32_t)D * 2u);
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)K, 0, stream_bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)V, 0, stream_bytes, kBufferFlags);
+  uint32_t k_voff[KvTile<D>::kDma], v_voff[KvTile<D>::kDma];
+  kv_offsets<D, true>(k_voff);
+  kv_offsets<D, false>(v_voff);
 
   uint32_t key_end = key_rows;
   if (Causal) {
-    const uint32_t last_q = (q0 + kQueriesPerBlock < query_rows ? q0 + kQueriesPerBlock : query_rows);
+    const uint32_t last_q = q0 + kQueriesPerBlock < query_rows ? q0 + kQueriesPerBlock : query_rows;
     key_end = last_q < key_rows ? last_q : key_rows;  // keys <= last query
   }
   const uint32_t nblocks = (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
-  const uint32_t wave_last_q = wq0 + 63;
+  constexpr uint32_t kBlockBytes = kKeysPerBlock * D * 2;
+  issue_kv<D>(k_rsrc, v_rsrc, lds_k0, lds_v0, k_voff, v_voff, 0);
 
-  KvRegs<D> regs;
-  load_kv<D>(K, V, 0, key_rows, regs);
-  store_kv<D>((smem + 0 + (0) * 2 * kBytes), (smem + kBytes + (0) * 2 * kBytes), regs);
-  __syncthreads();
+  // Q fragments (second MFMA operand): lane holds Q[q][16 ks + 8 (lane/32) ..+7].
+  half8_t qf[kKS];
+  {
+    uint32_t q = wq0 + lane % 32;
+    q = q < query_rows ? q : query_rows - 1;
+#pragma unroll
+    for (uint32_t ks = 0; ks < kKS; ++ks)
+      qf[ks] = __builtin_bit_cast(half8_t, load16(Q + (uint64_t)q * D + ks * 16 + (lane / 32) * 8));
+  }
 
-  for (uint32_t kbi = 0; kbi < nblocks; ++kbi) {
-    const uint32_t cur = kbi & 1;
+  float16_t o[kDT];
+#pragma unroll
+  for (uint32_t dt = 0; dt < kDT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  float m_run = -INFINITY;  // reference point, log2 units (scaled)
+  float l_run = 0.0f;       // this lane's share of the row sum
+  const uint32_t qi = wq0 + lane % 32;
+
+  auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi) {
+    // This wave's DMA of block kbi has landed (vmcnt(0)); after the barrier
+    // every wave's has, and every wave is done reading the other stage.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // The last block re-fetches itself into the stage that is no longer
+    // read: the DMA stays unconditional, which keeps the compiler's wait
+    // counting exact (no vmcnt wait before the reads of this stage).
+    const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
+    issue_kv<D>(k_rsrc, v_rsrc, nk, nv, k_voff, v_voff, next * kBlockBytes);
     const uint32_t kb = kbi * kKeysPerBlock;
-    const bool more = kbi + 1 < nblocks;
-    if (more) load_kv<D>(K, V, kb + kKeysPerBlock, key_rows, regs);
+    if (Causal && kb > wq0 + kQueriesPerWave - 1) return;
+    const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
 
-    const bool active = !Causal || kb <= wave_last_q;
-    if (active) {
-      const uint8_t* lk = (smem + 0 + (cur) * 2 * kBytes);
-      const uint8_t* lv = (smem + kBytes + (cur) * 2 * kBytes);
-      const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
+    // S^T for 64 keys x 32 queries: s[st][r] is key kb + 32 st + 8 (r/4) +
+    // 4 (lane/32) + r%4 of query qi.
+    float16_t s[2];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        // Scores S^T for 64 keys (two 32-key tiles) x 32 queries.
-        float16_t s[2];
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
+      for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
+    for (uint32_t ks = 0; ks < kKS; ++ks)
 #pragma unroll
-          for (uint32_t ks = 0; ks < kKS; ++ks) {
-            const half8_t kf = __builtin_bit_cast(
-                half8_t, *reinterpret_cast<const u32x4*>(
-                             lk + k_off<D>(st * 32 + lane % 32, ks * 2 + lane / 32)));
-            s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][ks], s[st], 0, 0, 0);
-          }
+      for (int st = 0; st < 2; ++st)
+        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k_frag<D>(lk, st, ks, lane), qf[ks], s[st], 0, 0, 0);
+
+    if (need_mask) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t kj = kb + 32 * st + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+          if ((Causal && kj > qi) || kj >= key_rows) s[st][r] = -INFINITY;
         }
-        // s[st][r] is key kb + 32 st + 8 (r/4) + 4 (lane/32) + r%4 of query
-        // wq0 + 32 qt + lane % 32.
-        const uint32_t qi = wq0 + qt * 32 + lane % 32;
-        float mx = -INFINITY;
+    }
+    float mx = s[0][0];
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float v = s[st][r] * scale_log2;
-            if (need_mask) {
-              const uint32_t kj = kb + 32 * st + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-              if ((Causal && kj > qi) || kj >= key_rows) v = -INFINITY;
-            }
-            s[st][r] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float m_new = fmaxf(m_run[qt], mx);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2f(m_run[qt] - m_use);
-        m_run[qt] = m_new;
-        float psum = 0.0f;
-        half8_t pf[2][2];
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * scale_log2;
+    // Every processed block holds at least one allowed key per query, so mx
+    // is finite; the reference point moves only by more than the slack.
+    if (__any(mx > m_run + kRescaleSlack)) {
+      const float m_new = mx > m_run + kRescaleSlack ? mx : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+      for (uint32_t dt = 0; dt < kDT; ++dt)
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+    }
+    const float neg_m = -m_run;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float p = exp2f(s[st][8 * h + e] - m_use);
-              psum += p;
-              pf[st][h][e] = (half_t)p;
-            }
-        l_run[qt] = l_run[qt] * alpha + psum;
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t pf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
+          l_run += p;
+          pf[e] = (half_t)p;
+        }
 #pragma unroll
         for (uint32_t dt = 0; dt < kDT; ++dt)
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_frag<D>(lv, st, h, dt, lane), pf, o[dt], 0, 0, 0);
+      }
+  };
+
+  uint32_t kbi = 0;
+  for (; kbi + 1 < nblocks; kbi += 2) {
+    step(lds_k0, lds_v0, lds_k1, lds_v1, kbi);
+    step(lds_k1, lds_v1, lds_k0, lds_v0, kbi + 1);
+  }
+  if (kbi < nblocks) step(lds_k0, lds_v0, lds_k1, lds_v1, kbi);
+  // Drain the last (redundant) DMA before the workgroup can exit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // o[dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][qi], unnormalised.
+  const float l_total = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = 1.0f / l_total;
+  if (qi >= query_rows) return;
+  const uint64_t row = ((uint64_t)stream * query_rows + qi) * D;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) o[qt][dt][e] *= alpha;
-        // O^T += V^T P^T over the 64 keys: 4 MFMAs (st, h) per d tile.
+  for (uint32_t dt = 0; dt < kDT; ++dt)
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
+      if constexpr (OutF16) {
+        half4_t hv;
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+        for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][4 * g + e] * inv);
+        *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
+      } else {
+        float4_t fv;
 #pragma unroll
-            for (uint32_t dt = 0; dt < kDT; ++dt) {
-              const half8_t vf = __builtin_bit_cast(
-                  half8_t, *reinterpret_cast<const u32x4*>(
-                               lv + vt_off(dt * 32 + lane % 32, st * 4 + h * 2 + lane / 32)));
-              o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[st][h], o[qt][dt], 0, 0, 0);
-            }
+        for (int e = 0; e < 4; ++e) fv[e] = o[dt][4 * g + e] * inv;
+        *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
       }
     }
-    if (more) store_kv<D>((smem + 0 + (cur ^ 1) * 2 * kBytes), (smem + kBytes + (cur ^ 1) * 2 * kBytes), regs);
-    __syncthreads();
-  }
-
-  // o[qt][dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][q].
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float l_total = l_run[qt] + __shfl_xor(l_run[qt], 32, kWave);
-    const float inv = 1.0f / l_total;
-    const uint32_t q = wq0 + qt * 32 + lane % 32;
-    if (q >= query_rows) continue;
-    const uint64_t row = ((uint64_t)stream * query_rows + q) * D;
-#pragma unroll
-    for (uint32_t dt = 0; dt < kDT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
-        if constexpr (OutF16) {
-          half4_t hv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[qt][dt][4 * g + e] * inv);
-          *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
-        } else {
-          float4_t fv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) fv[e] = o[qt][dt][4 * g + e] * inv;
-          *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
-        }
-      }
-  }
 }
 
 // General attention: one 64-lane block per (stream, query row); any widths.
@@ -379,7 +395,10 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   const float scale_log2 = a.scale * kLog2e;
   const bool aligned = ((uintptr_t)a.query % 16 == 0) && ((uintptr_t)a.key % 16 == 0) &&
                        ((uintptr_t)a.value % 16 == 0) && ((uintptr_t)a.out % 16 == 0);
-  if (aligned && a.width == a.value_width && (a.width == 128 || a.width == 64)) {
+  // The fast kernel addresses one stream's K or V through a buffer
+  // descriptor with a 31-bit byte range.
+  const bool fits = (uint64_t)a.key_rows * a.width * 2 <= 0x7fff0000ull;
+  if (aligned && fits && a.width == a.value_width && (a.width == 128 || a.width == 64)) {
     return a.width == 128 ? dispatch_fast<128>(stream, a, scale_log2)
                           : dispatch_fast<64>(stream, a, scale_log2);
   }
