@@ -82,6 +82,14 @@ __device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
   return row * KvTile<D>::kRowBytes + ((chunk ^ v_swz<D>(row)) << 4);
 }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// max / sum of x over lanes l and l ^ 32 (one ds_bpermute exchange).
+__device__ __forceinline__ float max_with_partner(float x) {
+  return fmaxf(x, __shfl_xor(x, 32, kWave));
+}
+__device__ __forceinline__ float sum_with_partner(float x) { return x + __shfl_xor(x, 32, kWave); }
+
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)lds, 16, voffset, 0, 0, 0);
 }
@@ -228,11 +236,15 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
+    // Raised priority while this wave feeds the matrix pipe: the other wave
+    // on the SIMD fills the gaps with its softmax.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (uint32_t ks = 0; ks < kKS; ++ks)
 #pragma unroll
       for (int st = 0; st < 2; ++st)
         s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k_frag<D>(lk, st, ks, lane), qf[ks], s[st], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
 
     if (need_mask) {
 #pragma unroll
@@ -248,7 +260,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * scale_log2;
+    mx = max_with_partner(mx) * scale_log2;
     // Every processed block holds at least one allowed key per query, so mx
     // is finite; the reference point moves only by more than the slack.
     if (__any(mx > m_run + kRescaleSlack)) {
@@ -268,11 +280,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
       for (int h = 0; h < 2; ++h) {
         half8_t pf;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
-          l_run += p;
-          pf[e] = (half_t)p;
-        }
+        for (int e = 0; e < 8; ++e)
+          pf[e] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
+        // The row sum adds the fp16 probabilities that the MFMA consumes, in
+        // fp32 (v_dot2 with ones: exact products, fp32 accumulation).
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          l_run = __builtin_amdgcn_fdot2(half2_t{pf[e], pf[e + 1]}, half2_t{1, 1}, l_run, false);
 #pragma unroll
         for (uint32_t dt = 0; dt < kDT; ++dt)
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_frag<D>(lv, st, h, dt, lane), pf, o[dt], 0, 0, 0);
@@ -289,7 +303,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // o[dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][qi], unnormalised.
-  const float l_total = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_total = sum_with_partner(l_run);
   const float inv = 1.0f / l_total;
   if (qi >= query_rows) return;
   const uint64_t row = ((uint64_t)stream * query_rows + qi) * D;
