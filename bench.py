@@ -102,6 +102,9 @@ def bench_memory_chain(ipus, ctx, steps, warmup, n=8192, sets=3):
     bm = [ctx.alloc(n * n * 2) for _ in range(sets)]
     r = ctx.alloc(n * 4)
     out = {}
+    out["copy"] = timed(
+        ctx, lambda i: ctx.launch("ipu_stack_copy", t[i % sets], [x[i % sets]], [n * n * 2]),
+        steps, warmup)
     out["transpose"] = timed(
         ctx, lambda i: ctx.launch("ipu_stack_transpose_f16", t[i % sets], [x[i % sets]], [1, n, n]),
         steps, warmup)
@@ -227,6 +230,69 @@ def committed_traffic():
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+LEGS = ("mfma_calibration", "gemm_f32_4096", "gemm_f16_256", "attention_causal_s4096",
+        "attention_noncausal_s2048", "memory_chain", "gelu_4096x16384", "mlp_graph")
+
+
+def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
+    """The other BASELINE configurations (results{} of the JSON line); `only`
+    restricts the run to the named legs (for profiling one kernel)."""
+    def want(name):
+        return only is None or name in only
+
+    n = 8192
+    results = {}
+    sub_steps = max(5, args.steps // 2)
+    if want("mfma_calibration"):
+        cal = mfma_calibration(ipus, ctx)
+        if headline_tflops:
+            cal["headline_frac_of_uniform"] = round(headline_tflops / cal["uniform"]["tflops"], 4)
+        results["mfma_calibration"] = cal
+        log(f"mfma calibration: {cal}")
+    if want("gemm_f32_4096"):
+        ms32 = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2)
+        t32 = 2.0 * 4096 ** 3 / (ms32 * 1e-3) / 1e12
+        results["gemm_f32_4096"] = {"ms": round(ms32, 5), "tflops": round(t32, 2),
+                                    "frac_peak": round(t32 / PEAK_FP32_TFLOPS, 4)}
+        log(f"gemm_f32 4096^3: {ms32:.4f} ms {t32:.1f} TFLOP/s")
+    if want("gemm_f16_256"):
+        ms256 = bench_gemm_f16(ipus, ctx, 256, 50, 5)
+        results["gemm_f16_256"] = {"ms": round(ms256, 5),
+                                   "tflops": round(2.0 * 256 ** 3 / (ms256 * 1e-3) / 1e12, 3)}
+    for causal, s in ((True, 4096), (False, 2048)):
+        key = f"attention_{'causal' if causal else 'noncausal'}_s{s}"
+        if not want(key):
+            continue
+        msa = bench_attention(ipus, ctx, s, causal, sub_steps, 2)
+        fl = 4.0 * 128 * 128 * (s * (s + 1) / 2 if causal else s * s)
+        ta = fl / (msa * 1e-3) / 1e12
+        results[key] = {"ms": round(msa, 5), "tflops": round(ta, 2),
+                        "frac_peak": round(ta / PEAK_FP16_TFLOPS, 4)}
+        log(f"{key}: {msa:.4f} ms {ta:.1f} TFLOP/s")
+    if want("memory_chain"):
+        chain = bench_memory_chain(ipus, ctx, args.steps, 3)
+        bytes_rw = {"copy": 2 * n * n * 2, "transpose": 2 * n * n * 2, "block_major": 2 * n * n * 2,
+                    "reduce_rows": n * n * 2 + n * 4, "reduce_rows_row_major": n * n * 2 + n * 4}
+        for k, v in chain.items():
+            gbps = bytes_rw[k] / (v * 1e-3) / 1e9
+            results[k] = {"ms": round(v, 5), "gbps": round(gbps, 1),
+                          "frac_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+            log(f"{k}: {v * 1e3:.1f} us {gbps:.0f} GB/s")
+    if want("gelu_4096x16384"):
+        msg = bench_gelu(ipus, ctx, args.steps, 3)
+        gg = 2 * 4096 * 16384 * 2 / (msg * 1e-3) / 1e9
+        results["gelu_4096x16384"] = {"ms": round(msg, 5), "gbps": round(gg, 1),
+                                      "frac_peak": round(gg / PEAK_HBM_GBPS, 4)}
+        log(f"gelu: {msg * 1e3:.1f} us {gg:.0f} GB/s")
+    if want("mlp_graph"):
+        msm = bench_mlp_graph(ipus, ctx, 5, 1)
+        tm = 2 * 2.0 * 4096 * 4096 * 16384 / (msm * 1e-3) / 1e12
+        results["mlp_graph"] = {"ms": round(msm, 5), "tflops": round(tm, 2),
+                                "frac_peak": round(tm / PEAK_FP16_TFLOPS, 4)}
+        log(f"mlp graph: {msm:.3f} ms {tm:.1f} TFLOP/s")
+    return results
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -236,6 +302,8 @@ def main() -> int:
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the headline GEMM and a calibration copy (for --pmc)")
+    ap.add_argument("--leg", action="append", choices=LEGS,
+                    help="run only these secondary legs (no headline; for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -254,6 +322,11 @@ def main() -> int:
         traffic_probe(ipus, ctx)
         ctx.close()
         return 0
+    if args.leg:
+        legs = secondary_legs(ipus, ctx, args, only=set(args.leg))
+        ctx.close()
+        print(json.dumps({"legs": legs}), flush=True)
+        return 0
 
     n = 8192
     flops = 2.0 * n ** 3
@@ -265,45 +338,7 @@ def main() -> int:
     results = {"gemm_f16_8192": {"ms": round(ms, 5), "tflops": round(tflops, 2),
                                  "frac_peak": round(tflops / PEAK_FP16_TFLOPS, 4)}}
     if not args.only_headline:
-        cal = mfma_calibration(ipus, ctx)
-        cal["headline_frac_of_uniform"] = round(tflops / cal["uniform"]["tflops"], 4)
-        results["mfma_calibration"] = cal
-        log(f"mfma calibration: {cal}")
-        sub_steps = max(5, args.steps // 2)
-        ms32 = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2)
-        t32 = 2.0 * 4096 ** 3 / (ms32 * 1e-3) / 1e12
-        results["gemm_f32_4096"] = {"ms": round(ms32, 5), "tflops": round(t32, 2),
-                                    "frac_peak": round(t32 / PEAK_FP32_TFLOPS, 4)}
-        log(f"gemm_f32 4096^3: {ms32:.4f} ms {t32:.1f} TFLOP/s")
-        ms256 = bench_gemm_f16(ipus, ctx, 256, 50, 5)
-        results["gemm_f16_256"] = {"ms": round(ms256, 5),
-                                   "tflops": round(2.0 * 256 ** 3 / (ms256 * 1e-3) / 1e12, 3)}
-        for causal, s in ((True, 4096), (False, 2048)):
-            msa = bench_attention(ipus, ctx, s, causal, sub_steps, 2)
-            fl = 4.0 * 128 * 128 * (s * (s + 1) / 2 if causal else s * s)
-            ta = fl / (msa * 1e-3) / 1e12
-            key = f"attention_{'causal' if causal else 'noncausal'}_s{s}"
-            results[key] = {"ms": round(msa, 5), "tflops": round(ta, 2),
-                            "frac_peak": round(ta / PEAK_FP16_TFLOPS, 4)}
-            log(f"{key}: {msa:.4f} ms {ta:.1f} TFLOP/s")
-        chain = bench_memory_chain(ipus, ctx, args.steps, 3)
-        bytes_rw = {"transpose": 2 * n * n * 2, "block_major": 2 * n * n * 2,
-                    "reduce_rows": n * n * 2 + n * 4, "reduce_rows_row_major": n * n * 2 + n * 4}
-        for k, v in chain.items():
-            gbps = bytes_rw[k] / (v * 1e-3) / 1e9
-            results[k] = {"ms": round(v, 5), "gbps": round(gbps, 1),
-                          "frac_peak": round(gbps / PEAK_HBM_GBPS, 4)}
-            log(f"{k}: {v * 1e3:.1f} us {gbps:.0f} GB/s")
-        msg = bench_gelu(ipus, ctx, args.steps, 3)
-        gg = 2 * 4096 * 16384 * 2 / (msg * 1e-3) / 1e9
-        results["gelu_4096x16384"] = {"ms": round(msg, 5), "gbps": round(gg, 1),
-                                      "frac_peak": round(gg / PEAK_HBM_GBPS, 4)}
-        log(f"gelu: {msg * 1e3:.1f} us {gg:.0f} GB/s")
-        msm = bench_mlp_graph(ipus, ctx, 5, 1)
-        tm = 2 * 2.0 * 4096 * 4096 * 16384 / (msm * 1e-3) / 1e12
-        results["mlp_graph"] = {"ms": round(msm, 5), "tflops": round(tm, 2),
-                                "frac_peak": round(tm / PEAK_FP16_TFLOPS, 4)}
-        log(f"mlp graph: {msm:.3f} ms {tm:.1f} TFLOP/s")
+        results.update(secondary_legs(ipus, ctx, args, tflops))
 
     line = {
         "metric": METRIC,
