@@ -5,32 +5,33 @@
 // evaluator's fp32 sgemm followed by one fp16 rounding
 // (crates/ipu-tests/src/diagnostic.rs:533-654, 841-847).
 //
-// Fast kernel (M % 256 == 0, N % 256 == 0, K % BK == 0):
-//   * block tile 256 x 256 x BK, 256 threads = 4 waves in a 2 x 2 grid, each
+// Fast kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0):
+//   * block tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each
 //     wave owns 128 x 128 of C as 4 x 4 tiles of v_mfma_f32_32x32x16_f16;
 //   * operand tiles go global -> LDS with buffer_load ... lds (16 bytes per
 //     lane, no staging registers; out-of-range reads return 0 instead of
 //     faulting).  The DMA writes lane i at base + 16 i, so the LDS swizzle is
 //     produced by choosing which global chunk each lane fetches;
 //   * an operand whose rows are K-contiguous in memory is stored as
-//     [256 rows][BK k] and read with ds_read_b128;
+//     [256 rows][64 k] and read with ds_read_b128;
 //   * an operand whose rows are M/N-contiguous (row-major B, transposed A) is
-//     stored as [BK k][256 mn] (512-byte rows) and read with
+//     stored as [64 k][256 mn] (512-byte rows) and read with
 //     ds_read_b64_tr_b16: in each 16-lane group, source lane s points at row
 //     k + s/4, column n + 4 (s % 4), and every lane receives 4 consecutive k
 //     of its own column, which is the MFMA fragment layout;
 //   * both swizzles are free of bank conflicts for 32 banks x 4 bytes and for
 //     64 banks x 4 bytes (the XOR patterns below are checked for both);
-//   * kStages LDS stages, each a distinct LDS object: the DMA for K step
-//     kt + kStages - 1 is in flight while step kt is multiplied; fragments are
-//     double-buffered in registers; one raw s_barrier per K step;
+//   * two LDS stages, each a distinct LDS object; BK = 64 is four 16-k
+//     substeps whose fragments are double-buffered in registers.  All reads
+//     of a stage are issued during its first three substeps, so the one
+//     raw s_barrier per K step sits before the fourth: that substep's MFMAs
+//     cover the DMA for step + 2 (into the stage just released) and the
+//     first fragment reads of step + 1;
 //   * the MFMA computes the tile of C^T (B fragment as the first operand) so
 //     each lane holds 4 consecutive columns of one row of C (one 8-byte store);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
 //     dispatch over 8 XCDs) form a compact group of C tiles sharing L2.
 // General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
-#include <cstdlib>
-
 #include "../../include/ipus.h"
 #include "device_common.h"
 #include "kernels.h"
@@ -54,12 +55,8 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HI
 // them in distinct bank groups under both.
 template <int BK>
 __device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t chunk) {
-  if constexpr (BK == 64) {  // 128-byte rows, 8 chunks
-    return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
-  } else {                   // 64-byte rows, 4 chunks
-    static_assert(BK == 32, "BK is 32 or 64");
-    return row * 64u + ((chunk ^ (((row >> 1) + (row >> 3)) & 3u)) << 4);
-  }
+  static_assert(BK == 64, "128-byte rows, 8 chunks");
+  return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
 }
 // MN-contiguous tile [BK k][256 mn]: byte offset of (k, 16-byte chunk along
 // mn).  A transposed read covers rows k..k+3 (k % 4 == 0) and 4 chunks (32
@@ -136,24 +133,20 @@ __device__ __forceinline__ half8_t read_frag(const uint8_t* tile, uint32_t row0,
   }
 }
 
-template <bool TransposeLeft, bool TransposeRight, int BK, int kStages>
+template <bool TransposeLeft, bool TransposeRight>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
     uint64_t left_batch_stride, uint64_t right_batch_stride) {
-  static_assert(kStages == 2 || kStages == 4, "2 or 4 stages");
-  static_assert(kStages * 2 * Tile<BK>::kBytes <= 160 * 1024, "LDS budget");
+  constexpr int BK = 64;
   constexpr int kTileBytes = Tile<BK>::kBytes;
   constexpr int kDma = Tile<BK>::kDmaPerWave;
-  // Stages are distinct LDS objects (unused ones are not allocated).
+  // The two stages are distinct LDS objects: the compiler can then see that
+  // a DMA into one never aliases the fragment reads of the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_a0[kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_b0[kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_a1[kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_b1[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a2[kStages == 4 ? kTileBytes : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b2[kStages == 4 ? kTileBytes : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a3[kStages == 4 ? kTileBytes : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b3[kStages == 4 ? kTileBytes : 16];
   constexpr bool kAK = !TransposeLeft;  // A rows (m) K-contiguous
   constexpr bool kBK_ = TransposeRight; // B^T rows (n) K-contiguous
 
@@ -209,91 +202,71 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
     issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
   };
-  // Prologue: K steps 0 .. kStages-2 (clamped: a short K re-fetches its last
-  // step into stages that are never read).
+  // Prologue: K steps 0 and 1 (clamped: K = 64 re-fetches step 0 into a
+  // stage that is never read).
   fetch(lds_a0, lds_b0, 0);
-  if constexpr (kStages == 4) {
-    fetch(lds_a1, lds_b1, clamp(1));
-    fetch(lds_a2, lds_b2, clamp(2));
-  }
+  fetch(lds_a1, lds_b1, clamp(1));
 
-  // One K step: multiply stage kt % kStages while K step kt + kStages - 1 is
-  // fetched into the stage freed by step kt - 1.  Distinct LDS objects and
-  // the unrolled loop let the compiler see that the DMA target never aliases
-  // the fragment reads.
-  auto step = [&](const uint8_t* ta, const uint8_t* tb, uint8_t* na, uint8_t* nb, uint32_t kt) {
-    // A raw s_barrier: __syncthreads() would add a workgroup fence, which
-    // drains every outstanding DMA (vmcnt(0)) and defeats the prefetch.
-    // The vmcnt wait leaves the younger stages' DMA in flight; lgkmcnt(0)
-    // retires this wave's fragment reads of step kt - 1 before any wave may
-    // overwrite that stage; the asm is also a compiler barrier for the LDS
-    // accesses around it.
-    if constexpr (kStages == 4) {
-      static_assert(kStages != 4 || 2 * 2 * kDma == 16, "vmcnt immediate below");
-      asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // 4 substeps of 16 k.  Substep s multiplies buffer
+  // s % 2 while the fragments of substep s + 1 are read; every read of the
+  // current stage is issued during substeps 0..2, so the per-step barrier
+  // sits before substep 3, whose MFMAs then cover the DMA of step kt + 2
+  // (into the stage just released) and the reads of step kt + 1's first
+  // substep.
+  half8_t fa[2][4], fb[2][4];
+  constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
+  auto read_sub = [&](const uint8_t* ta, const uint8_t* tb, uint32_t ks, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[buf][i] = read_frag<BK, kAK>(ta, wm + 32 * i, ks, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[buf][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, ks, lane);
+  };
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+  };
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  read_sub(lds_a0, lds_b0, 0, 0);
+  auto step = [&](uint8_t* ta, uint8_t* tb, const uint8_t* na, const uint8_t* nb, uint32_t kt) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      read_sub(ta, tb, s + 1, (s + 1) % 2);
+      mma(s % 2);
     }
-    // The last steps re-fetch step ksteps - 1 into stages that are never
-    // read, keeping the body one branch-free scheduling region; the
-    // outstanding DMA is drained after the loop.
-    fetch(na, nb, clamp(kt + kStages - 1));
-    half8_t fa[2][4], fb[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[0][i] = read_frag<BK, kAK>(ta, wm + 32 * i, 0, lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) fb[0][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, 0, lane);
-#pragma unroll
-    for (uint32_t ks = 0; ks < BK / 16; ++ks) {
-      const uint32_t cur = ks & 1;
-      if (ks + 1 < BK / 16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) fa[cur ^ 1][i] = read_frag<BK, kAK>(ta, wm + 32 * i, ks + 1, lane);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) fb[cur ^ 1][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, ks + 1, lane);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
-    }
-    // Issue order: the first substep's fragment reads, then each MFMA
-    // followed by one fragment read of the next substep (and, during the
-    // first substep, one prefetch DMA), so LDS and memory latency hide under
-    // the matrix pipe.
-    constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
-    constexpr int kSubs = BK / 16;
-    __builtin_amdgcn_sched_group_barrier(0x100, kDsPerSub, 0);
-#pragma unroll
-    for (int sub = 0; sub < kSubs; ++sub) {
+    for (int s = 0; s < 3; ++s) {
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (sub == 0 && m < 2 * kDma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        if (sub + 1 < kSubs && m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // This wave's reads of (ta, tb) have returned and its DMA of step kt + 1
+    // has landed; after the barrier, every wave's have.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(ta, tb, clamp(kt + 2));
+    read_sub(na, nb, 0, 0);
+    mma(1);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (m < 2 * kDma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   };
 
   uint32_t kt = 0;
-  if constexpr (kStages == 4) {
-    for (; kt + 3 < ksteps; kt += 4) {
-      step(lds_a0, lds_b0, lds_a3, lds_b3, kt);
-      step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
-      step(lds_a2, lds_b2, lds_a1, lds_b1, kt + 2);
-      step(lds_a3, lds_b3, lds_a2, lds_b2, kt + 3);
-    }
-    if (kt < ksteps) step(lds_a0, lds_b0, lds_a3, lds_b3, kt);
-    if (kt + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
-    if (kt + 2 < ksteps) step(lds_a2, lds_b2, lds_a1, lds_b1, kt + 2);
-  } else {
-    for (; kt + 1 < ksteps; kt += 2) {
-      step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
-      step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
-    }
-    if (kt < ksteps) step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
+  for (; kt + 1 < ksteps; kt += 2) {
+    step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
+    step(lds_a1, lds_b1, lds_a0, lds_b0, kt + 1);
   }
+  if (kt < ksteps) step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the redundant prefetches
 
   // acc[i][j][r] = C[m0 + wm + 32 i + lane % 32][n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4]
@@ -358,31 +331,20 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
   }
 }
 
-template <bool TL, bool TR, int BK, int S>
+template <bool TL, bool TR>
 int launch_fast(hipStream_t stream, const GemmArgs& a) {
   const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
-  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, BK, S>), dim3(tiles, a.batches), dim3(kThreads),
-                     0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
-                     (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
-                     a.right_batch_stride);
+  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR>), dim3(tiles, a.batches), dim3(kThreads), 0,
+                     stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
+                     a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
   return hip_status(hipGetLastError());
 }
 
-template <int BK, int S>
 int dispatch_fast(hipStream_t stream, const GemmArgs& a) {
-  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false, BK, S>(stream, a);
-  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true, BK, S>(stream, a);
-  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false, BK, S>(stream, a);
-  return launch_fast<true, true, BK, S>(stream, a);
-}
-
-// Pipeline variant: 0 = BK 64 x 2 stages, 1 = BK 32 x 4 stages.
-int pipeline_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("IPUS_GEMM_F16_PIPELINE");
-    return e ? std::atoi(e) : 0;
-  }();
-  return v;
+  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
+  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
+  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);
+  return launch_fast<true, true>(stream, a);
 }
 
 }  // namespace
@@ -398,10 +360,7 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
   const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
   if (aligned && fits && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner > 0) {
-    const int v = pipeline_variant();
-    if (v == 1 && a.inner % 32 == 0) return dispatch_fast<32, 4>(stream, a);
-    if (a.inner % 64 == 0) return dispatch_fast<64, 2>(stream, a);
-    if (a.inner % 32 == 0) return dispatch_fast<32, 4>(stream, a);
+    if (a.inner % 64 == 0) return dispatch_fast(stream, a);
   }
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
