@@ -19,8 +19,7 @@
  *
  * Conventions (kernel.rs:14-16, crates/ipu-codegen/src/operator.rs:467-537):
  *   - The caller owns every buffer.  Kernels read inputs and write the output
- *     and allocate nothing (the row reduction's partial sums use a per-context
- *     workspace that the context owns).
+ *     and allocate nothing.
  *   - Launches are ordered on the context's stream (replacing BSP phases).
  *   - Every call returns 0 on success or a negative IPUS_ERROR_* code;
  *     ipus_last_error() returns the message of the calling thread's last
@@ -108,6 +107,11 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        left_batch_stride, right_batch_stride  (strides in elements, 0 =
  *        broadcast).  Replaces gemm_f16_amp (device/gemm_f16_amp.S:186-440)
  *        with fp32 accumulation and fp16 output.
+ *   ipu_stack_gemm_f16_gelu            as ipu_stack_gemm_f16, then the tanh
+ *        GELU of each fp16 result element (bit-identical to
+ *        ipu_stack_gemm_f16 followed by ipu_stack_gelu_tanh_approx_f16).  No
+ *        reference symbol: build_package fuses a Gemm whose result feeds only
+ *        one Gelu (graph.rs:315-331) into this launch.
  *   ipu_stack_gemm_f32                 as above in fp32
  *        (device/gemm_f32_64_amp.S:125-385).
  *   ipu_stack_flash_attention_online_f16  out (f32 or f16); query, key,

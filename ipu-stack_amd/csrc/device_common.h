@@ -64,4 +64,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// tanh-approximation GELU of one fp16 value widened to fp32 (the value the
+// reference's formula is applied to, crates/ipu-tests/src/main.rs:1985-1987):
+//   0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)),  u = 0.7978846 (x + 0.044715 x^3).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // x / (1 + exp(-2u)) with exp(-2u) = exp2(-2 log2(e) u): v_exp_f32 and
+  // v_rcp_f32 (about 1 ulp of fp32 each, far below the fp16 result's
+  // rounding); x -> -inf gives x * rcp(inf) = -0 as the exact form does.
+  constexpr float kA = -2.0f * 0.7978846f * 1.4426950408889634f;
+  const float t = x * x;
+  const float v = x * fmaf(t, 0.044715f, 1.0f);  // x + 0.044715 x^3
+  const float e = __builtin_amdgcn_exp2f(v * kA);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 }  // namespace ipus

@@ -860,6 +860,41 @@ struct Builder {
   }
 };
 
+// A Gemm whose whole fp16 result is read only by a Gelu of all of it
+// becomes one launch with GELU in the GEMM epilogue: the epilogue rounds
+// each product to fp16 and applies the GELU kernel's function to that
+// value, so the result is bit-identical and one 2-byte-per-element write
+// and read of the intermediate disappear.
+void fuse_gemm_gelu(ipus_package& pkg) {
+  std::vector<int> reads(pkg.slots.size(), 0), writes(pkg.slots.size(), 0);
+  for (const Step& s : pkg.steps) {
+    ++writes[(size_t)s.out.slot];
+    for (const Operand& o : s.ins) ++reads[(size_t)o.slot];
+  }
+  std::vector<Step> steps;
+  for (size_t i = 0; i < pkg.steps.size(); ++i) {
+    const Step& s = pkg.steps[i];
+    if (i + 1 < pkg.steps.size() && s.symbol == "ipu_stack_gemm_f16" && s.out.byte_offset == 0) {
+      const Step& n = pkg.steps[i + 1];
+      const int mid = s.out.slot;
+      const Slot& ms = pkg.slots[(size_t)mid];
+      if (n.symbol == "ipu_stack_gelu_tanh_approx_f16" && n.ins.size() == 1 &&
+          n.ins[0].slot == mid && n.ins[0].byte_offset == 0 && n.out.byte_offset == 0 &&
+          !ms.external && writes[(size_t)mid] == 1 && reads[(size_t)mid] == 1 &&
+          n.scalars[0] == elements(ms.storage.shape)) {
+        Step f = s;
+        f.symbol = "ipu_stack_gemm_f16_gelu";
+        f.out = n.out;
+        steps.push_back(std::move(f));
+        ++i;
+        continue;
+      }
+    }
+    steps.push_back(s);
+  }
+  pkg.steps = std::move(steps);
+}
+
 // Lifetime-packed arena offsets for non-external slots.
 uint64_t place(ipus_package& pkg) {
   for (size_t i = 0; i < pkg.steps.size(); ++i) {
@@ -945,6 +980,7 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
   }
   // Precision map (CompiledPackage::precisions) over every value bound to a slot.
   for (const auto& kv : b.env) pkg->precisions[kv.first] = pkg->slots[(size_t)kv.second].storage.precision;
+  fuse_gemm_gelu(*pkg);
   pkg->arena_bytes = place(*pkg);
   *out = pkg.release();
   return 0;

@@ -11,10 +11,6 @@
 struct ipus_context {
   int device = 0;
   hipStream_t stream = nullptr;
-  // Library-owned scratch (row-reduction partial sums).  Grows on demand.
-  void* workspace_ptr = nullptr;
-  size_t workspace_bytes = 0;
-  float* workspace(size_t bytes);
 };
 
 namespace ipus {

@@ -133,7 +133,17 @@ __device__ __forceinline__ half8_t read_frag(const uint8_t* tile, uint32_t row0,
   }
 }
 
-template <bool TransposeLeft, bool TransposeRight>
+// fp16 result of one accumulator; with Gelu, GELU of that fp16 value (the
+// same number the separate GELU kernel would produce from the stored GEMM
+// output).
+template <bool Gelu>
+__device__ __forceinline__ half_t epilogue(float acc) {
+  const half_t h = (half_t)acc;
+  if constexpr (Gelu) return (half_t)gelu_tanh((float)h);
+  return h;
+}
+
+template <bool TransposeLeft, bool TransposeRight, bool Gelu>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
@@ -280,7 +290,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
       for (int g = 0; g < 4; ++g) {
         half4_t h;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (half_t)acc[i][j][4 * g + e];
+        for (int e = 0; e < 4; ++e) h[e] = epilogue<Gelu>(acc[i][j][4 * g + e]);
         *reinterpret_cast<half4_t*>(crow + 32 * j + 8 * g) = h;
       }
     }
@@ -292,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr,
-    uint64_t left_batch_stride, uint64_t right_batch_stride, uint32_t tiles_n) {
+    uint64_t left_batch_stride, uint64_t right_batch_stride, uint32_t tiles_n, bool gelu) {
   __shared__ __attribute__((aligned(16))) half_t As[64][24];
   __shared__ __attribute__((aligned(16))) half_t Bs[64][24];
   const uint64_t batch = blockIdx.y;
@@ -327,24 +337,27 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const uint32_t n = n0 + wn + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-    if (n < N) C[(uint64_t)m * N + n] = __builtin_bit_cast(uint16_t, (half_t)acc[r]);
+    if (n < N)
+      C[(uint64_t)m * N + n] =
+          __builtin_bit_cast(uint16_t, gelu ? epilogue<true>(acc[r]) : epilogue<false>(acc[r]));
   }
 }
 
-template <bool TL, bool TR>
+template <bool TL, bool TR, bool G>
 int launch_fast(hipStream_t stream, const GemmArgs& a) {
   const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
-  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR>), dim3(tiles, a.batches), dim3(kThreads), 0,
+  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G>), dim3(tiles, a.batches), dim3(kThreads), 0,
                      stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
                      a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
   return hip_status(hipGetLastError());
 }
 
+template <bool G>
 int dispatch_fast(hipStream_t stream, const GemmArgs& a) {
-  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
-  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
-  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);
-  return launch_fast<true, true>(stream, a);
+  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false, G>(stream, a);
+  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true, G>(stream, a);
+  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false, G>(stream, a);
+  return launch_fast<true, true, G>(stream, a);
 }
 
 }  // namespace
@@ -360,13 +373,14 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
   const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
   if (aligned && fits && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner > 0) {
-    if (a.inner % 64 == 0) return dispatch_fast(stream, a);
+    if (a.inner % 64 == 0)
+      return a.gelu ? dispatch_fast<true>(stream, a) : dispatch_fast<false>(stream, a);
   }
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
                      stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
                      a.rows, a.columns, a.inner, a.transpose_left, a.transpose_right,
-                     a.left_batch_stride, a.right_batch_stride, tiles_n);
+                     a.left_batch_stride, a.right_batch_stride, tiles_n, a.gelu);
   return hip_status(hipGetLastError());
 }
 

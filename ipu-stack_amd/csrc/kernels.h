@@ -18,6 +18,7 @@ struct GemmArgs {
   uint64_t right_batch_stride;  // elements; 0 broadcasts one matrix
   uint32_t rows, columns, inner;
   bool transpose_left, transpose_right;
+  bool gelu = false;  // fp16 GEMM only: GELU of the fp16 result in the epilogue
 };
 
 struct AttentionArgs {
@@ -50,11 +51,9 @@ int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t s
                       uint32_t logical_columns, uint32_t physical_columns);
 // Row sums with fp32 accumulation of a logical [rows, columns] fp16 matrix
 // stored row-major (source_order = 3) or block-major (source_order = 2).
-// `workspace` must hold reduce_rows_workspace_bytes(...) bytes.
-size_t reduce_rows_workspace_bytes(uint32_t source_order, uint32_t rows, uint32_t columns);
 int launch_reduce_rows_f16(hipStream_t stream, float* dst, const void* src, uint32_t source_order,
                            uint32_t row_block, uint32_t column_block, uint32_t rows,
-                           uint32_t columns, float* workspace);
+                           uint32_t columns);
 int launch_reduce_sum_f16(hipStream_t stream, void* dst, const void* initial, const void* remote,
                           uint32_t remote_partials, uint32_t count);
 int launch_gelu_f16(hipStream_t stream, void* dst, const void* src, uint64_t count);

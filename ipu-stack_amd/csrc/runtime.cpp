@@ -56,20 +56,6 @@ int check_launch(int status, const char* symbol) {
 
 using namespace ipus;
 
-float* ipus_context::workspace(size_t bytes) {
-  if (bytes == 0) return nullptr;
-  if (bytes > workspace_bytes) {
-    if (workspace_ptr) {
-      hipStreamSynchronize(stream);
-      hipFree(workspace_ptr);
-      workspace_ptr = nullptr;
-      workspace_bytes = 0;
-    }
-    if (hipMalloc(&workspace_ptr, bytes) != hipSuccess) return nullptr;
-    workspace_bytes = bytes;
-  }
-  return (float*)workspace_ptr;
-}
 
 
 // ---------------------------------------------------------------------------
@@ -120,7 +106,6 @@ extern "C" int ipus_context_destroy(ipus_context* ctx) {
   if (!ctx) return 0;
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
-  if (ctx->workspace_ptr) hipFree(ctx->workspace_ptr);
   hipStreamDestroy(ctx->stream);
   delete ctx;
   return 0;
@@ -279,8 +264,10 @@ inline float bits_to_float(uint32_t bits) {
   return f;
 }
 
-int run_gemm(ipus_context* ctx, void* out, const void* const* in, const uint32_t* s, bool f16) {
+int run_gemm(ipus_context* ctx, void* out, const void* const* in, const uint32_t* s, bool f16,
+             bool gelu = false) {
   GemmArgs a;
+  a.gelu = gelu;
   a.out = out;
   a.left = in[0];
   a.right = in[1];
@@ -303,6 +290,15 @@ const std::vector<KernelEntry>& registry() {
         "left_batch_stride", "right_batch_stride"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return run_gemm(c, o, i, s, true);
+       }},
+      // Gemm followed by Gelu of its fp16 result, fused into the GEMM
+      // epilogue (no reference counterpart: build_package emits it for a
+      // Gemm whose result only feeds one Gelu).
+      {"ipu_stack_gemm_f16_gelu", 2,
+       {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
+        "left_batch_stride", "right_batch_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_gemm(c, o, i, s, true, true);
        }},
       {"ipu_stack_gemm_f32", 2,
        {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
@@ -363,14 +359,7 @@ const std::vector<KernelEntry>& registry() {
       {"ipu_stack_reduce_rows_f16", 1,
        {"rows", "columns", "source_order", "row_block", "column_block"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         float* ws = nullptr;
-         const size_t bytes = reduce_rows_workspace_bytes(s[2], s[0], s[1]);
-         if (bytes) {
-           ws = c->workspace(bytes);
-           if (!ws) return IPUS_ERROR_OUT_OF_MEMORY;
-         }
-         return launch_reduce_rows_f16(c->stream, (float*)o, i[0], s[2], s[3], s[4], s[0], s[1],
-                                       ws);
+         return launch_reduce_rows_f16(c->stream, (float*)o, i[0], s[2], s[3], s[4], s[0], s[1]);
        }},
       {"ipu_stack_fill_zero", 0, {"byte_count"},
        [](ipus_context* c, void* o, const void* const*, const uint32_t* s) {

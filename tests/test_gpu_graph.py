@@ -1,0 +1,163 @@
+"""GPU runs of compiled packages (build_package + session) against the CPU
+oracle, and the fused GEMM+GELU launch against its two-launch form.
+
+Each graph is built with the ComputeGraph API, compiled, bound and run on
+cuda:0; the expected values come from the oracle's restatement of the
+reference's per-operator evaluation (crates/ipu-tests/src/diagnostic.rs:
+411-847) applied step by step in the same precisions.  Bars as in
+test_gpu_kernels.py: bit-exact for rearranges and for the fusion against the
+unfused launches, normwise max-rel <= 1e-2 for fp16 results.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+
+FP16_TOL = 1e-2
+
+
+def synth(ipus, n, seed, tensor, dist=1, scale=1.0):
+    return ipus.synth_f16(n, seed, tensor, dist, scale)
+
+
+def run_package(ipus, ctx, graph, feeds, config=None):
+    pkg = ipus.build_package(graph, config)
+    sess = pkg.session(ctx)
+    for name, array in feeds.items():
+        sess.write(name, array)
+    sess.run_sync()
+    outs = [sess.read(t.name) for t in pkg.outputs]
+    sess.close()
+    return pkg, outs
+
+
+def test_mlp_package_matches_oracle_and_fusion_is_exact(ipus, oracle, ctx):
+    # configs[3]'s structure at a small size: X . W1 -> GELU -> . W2.
+    m, d, h = 256, 256, 1024
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [m, d])
+    w1 = g.parameter("w1", [d, h])
+    w2 = g.parameter("w2", [h, d])
+    g.set_outputs([g.gemm(g.gelu(g.gemm(x, w1)), w2)])
+    xs = synth(ipus, m * d, 31, 1).reshape(m, d)
+    w1s = synth(ipus, d * h, 31, 2, scale=0.05).reshape(d, h)
+    w2s = synth(ipus, h * d, 31, 3, scale=0.05).reshape(h, d)
+    pkg, (y,) = run_package(ipus, ctx, g, {"x": xs, "w1": w1s, "w2": w2s})
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16"]
+    hidden = oracle.gelu_f16(oracle.gemm_f16(xs, w1s, m, h, d)).reshape(m, h)
+    want = oracle.f16_to_f32(oracle.gemm_f16(hidden, w2s, m, d, h)).reshape(m, d)
+    assert max_rel(oracle.f16_to_f32(y), want) <= FP16_TOL
+    # The fused launch equals GEMM then GELU bit for bit.
+    bx, b1 = ctx.upload(xs), ctx.upload(w1s)
+    fused, plain, act = ctx.alloc(m * h * 2), ctx.alloc(m * h * 2), ctx.alloc(m * h * 2)
+    sc = [1, m, h, d, 0, 0, 0, 0]
+    ctx.launch("ipu_stack_gemm_f16_gelu", fused, [bx, b1], sc)
+    ctx.launch("ipu_stack_gemm_f16", plain, [bx, b1], sc)
+    ctx.launch("ipu_stack_gelu_tanh_approx_f16", act, [plain], [m * h])
+    assert np.array_equal(fused.download(np.uint16), act.download(np.uint16))
+    for b in (bx, b1, fused, plain, act):
+        b.free()
+
+
+@pytest.mark.parametrize("M,N,K,tl,tr", [(256, 512, 128, 0, 0), (512, 256, 192, 1, 1),
+                                         (100, 60, 40, 0, 0), (64, 96, 48, 0, 1)])
+def test_gemm_gelu_fusion_bit_exact(ipus, ctx, M, N, K, tl, tr):
+    a = synth(ipus, M * K, 32, 1)
+    b = synth(ipus, K * N, 32, 2, scale=0.2)
+    ba, bb = ctx.upload(a), ctx.upload(b)
+    fused, plain, act = ctx.alloc(M * N * 2), ctx.alloc(M * N * 2), ctx.alloc(M * N * 2)
+    sc = [1, M, N, K, tl, tr, 0, 0]
+    ctx.launch("ipu_stack_gemm_f16_gelu", fused, [ba, bb], sc)
+    ctx.launch("ipu_stack_gemm_f16", plain, [ba, bb], sc)
+    ctx.launch("ipu_stack_gelu_tanh_approx_f16", act, [plain], [M * N])
+    assert np.array_equal(fused.download(np.uint16), act.download(np.uint16))
+    for buf in (ba, bb, fused, plain, act):
+        buf.free()
+
+
+def test_attention_package_matches_oracle(ipus, oracle, ctx):
+    # Projections, head split and causal attention (graph.rs:338-362).
+    b, s, d, heads = 2, 128, 256, 2
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [b, s, d])
+    wq = g.parameter("wq", [d, d])
+    wk = g.parameter("wk", [d, d])
+    wv = g.parameter("wv", [d, d])
+    q = g.split_heads(g.gemm(x, wq), heads)
+    k = g.split_heads(g.gemm(x, wk), heads)
+    v = g.split_heads(g.gemm(x, wv), heads)
+    g.set_outputs([g.flash_attention_with_options(q, k, v, causal=True)])
+    xs = synth(ipus, b * s * d, 33, 1).reshape(b, s, d)
+    ws = {n: synth(ipus, d * d, 33, i + 2, scale=0.08).reshape(d, d)
+          for i, n in enumerate(("wq", "wk", "wv"))}
+    pkg, (o,) = run_package(ipus, ctx, g, {"x": xs, **ws})
+    assert o.dtype == np.float32 and o.shape == (b * heads, s, d // heads)
+    proj = {n: oracle.f16_to_f32(oracle.gemm_f16(xs.reshape(b * s, d), ws[n], b * s, d, d))
+            .reshape(b, s, d) for n in ws}
+    qh, kh, vh = (oracle.split_heads(proj[n], heads) for n in ("wq", "wk", "wv"))
+    want = oracle.attention(qh, kh, vh, b * heads, s, s, d // heads, d // heads, causal=True)
+    assert max_rel(o.reshape(-1, d // heads), want) <= FP16_TOL
+
+
+def test_memory_chain_package_bit_exact(ipus, oracle, ctx):
+    n = 512
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [n, n])
+    t = g.transpose(x)
+    bm = g.rearrange(t, ipus.ORDER_BLOCK_MAJOR, 64, 64)
+    r = g.reduce_rows(bm)
+    g.set_outputs([t, bm, r])
+    xs = synth(ipus, n * n, 34, 1).reshape(n, n)
+    _, (tg, bmg, rg) = run_package(ipus, ctx, g, {"x": xs})
+    tw = oracle.transpose_u16(xs, 1, n, n).reshape(n, n)
+    assert np.array_equal(tg, tw)
+    bmw = oracle.rearrange_row_major_f16(tw, 2, 1, n, n, n, n, 64, 64)
+    assert np.array_equal(bmg.reshape(-1), bmw.reshape(-1))
+    rw = oracle.reduce_rows_f16(tw, n, n)
+    assert np.abs(rg - rw).max() <= 1e-5 * max(1.0, np.abs(rw).max())
+
+
+def test_add_broadcast_and_f32_compute_package(ipus, oracle, ctx):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [4, 64, 32])
+    bias = g.parameter("bias", [32])
+    w = g.parameter("w", [32, 48])
+    y = g.gemm(g.add(x, bias), w)
+    g.set_outputs([y])
+    xs = synth(ipus, 4 * 64 * 32, 35, 1).reshape(4, 64, 32)
+    bs = synth(ipus, 32, 35, 2).reshape(32)
+    wsr = synth(ipus, 32 * 48, 35, 3, scale=0.2).reshape(32, 48)
+    # fp32 compute: host tensors are fp32 (PackageConfig compute precision)
+    cfg = ipus.PackageConfig(compute_precision="f32")
+    xf, bf, wf = (oracle.f16_to_f32(a) for a in (xs, bs, wsr))
+    _, (yf,) = run_package(ipus, ctx, g, {"x": xf, "bias": bf, "w": wf}, cfg)
+    want = oracle.add_f32(xf, bf).reshape(-1, 32) @ wf.astype(np.float64)
+    assert np.abs(yf.reshape(-1, 48) - want).max() <= 1e-5 * np.abs(want).max()
+    # fp16 compute: the add rounds to fp16 before the GEMM
+    _, (yh,) = run_package(ipus, ctx, g, {"x": xs, "bias": bs, "w": wsr})
+    added = oracle.f32_to_f16(oracle.add_f32(xf, bf)).reshape(-1, 32)
+    want16 = oracle.f16_to_f32(oracle.gemm_f16(added, wsr, 4 * 64, 48, 32)).reshape(4, 64, 48)
+    assert max_rel(oracle.f16_to_f32(yh), want16) <= FP16_TOL
+
+
+def test_repeat_package_matches_unrolled_oracle(ipus, oracle, ctx):
+    # x <- x + x . W_i for i in 0..3 (graph.rs:382-472, diagnostic.rs:466-522)
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [64, 64])
+    ws = [g.parameter(f"w{i}", [64, 64]) for i in range(4)]
+    seq = g.value_sequence("layers", ws)
+    out = g.repeat(4, [x], [], [seq],
+                   lambda body, a: [body.add(a.carried[0], body.gemm(a.carried[0], a.iterated[0]))])
+    g.set_outputs(out)
+    xs = synth(ipus, 64 * 64, 36, 1).reshape(64, 64)
+    wv = [synth(ipus, 64 * 64, 36, i + 2, scale=0.05).reshape(64, 64) for i in range(4)]
+    _, (y,) = run_package(ipus, ctx, g, {"x": xs, **{f"w{i}": wv[i] for i in range(4)}})
+    cur = xs
+    for w in wv:
+        prod = oracle.gemm_f16(cur, w, 64, 64, 64).reshape(64, 64)
+        cur = oracle.f32_to_f16(oracle.f16_to_f32(cur) + oracle.f16_to_f32(prod)).reshape(64, 64)
+    assert max_rel(oracle.f16_to_f32(y), oracle.f16_to_f32(cur)) <= FP16_TOL

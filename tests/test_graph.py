@@ -145,13 +145,39 @@ def test_build_package_mlp_plan(ipus):
     y = g.gemm(g.gelu(g.gemm(x, w1)), w2)
     g.set_outputs([y])
     pkg = ipus.build_package(g)
-    assert [s[0] for s in pkg.steps] == [
-        "ipu_stack_gemm_f16", "ipu_stack_gelu_tanh_approx_f16", "ipu_stack_gemm_f16"]
+    # The GELU of the first GEMM's result is fused into its epilogue.
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16"]
     assert pkg.steps[0][2][:4] == (1, 4096, 16384, 4096)
     assert [t.name for t in pkg.inputs] == ["input", "w1", "w2"]
     assert pkg.outputs[0].name == "output.0" and pkg.outputs[0].shape == (4096, 4096)
-    # hidden (128 MiB) and gelu(hidden) (128 MiB) are both live across the GELU
-    assert pkg.arena_bytes == 2 * 4096 * 16384 * 2
+    # only gelu(hidden) (128 MiB) lives in the arena
+    assert pkg.arena_bytes == 4096 * 16384 * 2
+
+
+def test_gemm_gelu_fusion_needs_a_private_result(ipus):
+    # The GEMM result is also an output: both launches stay.
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [256, 256])
+    w = g.parameter("w", [256, 256])
+    h = g.gemm(x, w)
+    g.set_outputs([g.gelu(h), h])
+    assert [s[0] for s in ipus.build_package(g).steps][:2] == [
+        "ipu_stack_gemm_f16", "ipu_stack_gelu_tanh_approx_f16"]
+    # The GEMM result has a second reader.
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [256, 256])
+    w = g.parameter("w", [256, 256])
+    h = g.gemm(x, w)
+    g.set_outputs([g.add(g.gelu(h), h)])
+    steps = [s[0] for s in ipus.build_package(g).steps]
+    assert steps[:2] == ["ipu_stack_gemm_f16", "ipu_stack_gelu_tanh_approx_f16"]
+    # fp32 compute: the GEMM result is cast before the GELU, no fusion.
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [256, 256])
+    w = g.parameter("w", [256, 256])
+    g.set_outputs([g.gelu(g.gemm(x, w))])
+    steps = [s[0] for s in ipus.build_package(g, ipus.PackageConfig(compute_precision="f32")).steps]
+    assert "ipu_stack_gemm_f16_gelu" not in steps
 
 
 def test_build_package_arena_reuses_dead_values(ipus):
