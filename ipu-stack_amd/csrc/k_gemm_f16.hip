@@ -188,7 +188,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)b_base, 0, (int)(b_bytes > 0x7fffffffull ? 0x7fffffff : b_bytes), kBufferFlags);
 
-  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  // wave is uniform: readfirstlane puts it in an SGPR, so the LDS
+  // addresses of the DMA (M0) are scalar arithmetic.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t lane = threadIdx.x % kWave;
   uint32_t a_voff[kDma], b_voff[kDma];
   tile_offsets<BK, kAK>(wave, lane, kAK ? K : M, a_voff);
   tile_offsets<BK, kBK_>(wave, lane, kBK_ ? K : N, b_voff);
