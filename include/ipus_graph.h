@@ -146,6 +146,14 @@ int ipus_session_read(ipus_session *session, const char *name, void *host, size_
 int ipus_session_tensor_pointer(ipus_session *session, const char *name, void **device_pointer);
 /* Enqueues every step on the context stream (asynchronous). */
 int ipus_session_run(ipus_session *session);
+/* Records the package's launches on the context stream into a HIP graph;
+ * every later ipus_session_run replays it with one hipGraphLaunch (the
+ * buffers are the session's, so ipus_session_write between runs feeds the
+ * replay).  The role of the reference's precompiled device program
+ * (HostSession runs, crates/ipu-driver/src/lib.rs:1341-1600) for
+ * launch-bound packages; no reference function of its own.  Every step is
+ * a kernel (no memset nodes).  A second call is a no-op. */
+int ipus_session_capture(ipus_session *session);
 
 #ifdef __cplusplus
 }

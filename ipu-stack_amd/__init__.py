@@ -202,6 +202,7 @@ _SIGNATURES = {
     "ipus_session_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, ctypes.c_size_t]),
     "ipus_session_tensor_pointer": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(_P)]),
     "ipus_session_run": (ctypes.c_int, [_P]),
+    "ipus_session_capture": (ctypes.c_int, [_P]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -723,6 +724,10 @@ class Session:
 
     def run(self) -> None:
         _check(_lib().ipus_session_run(self.handle))
+
+    def capture(self) -> None:
+        """Record the package's launches as a HIP graph; later runs replay it."""
+        _check(_lib().ipus_session_capture(self.handle))
 
     def run_sync(self) -> None:
         self.run()

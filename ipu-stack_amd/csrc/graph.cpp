@@ -1065,6 +1065,9 @@ struct ipus_session {
   const ipus_package* pkg = nullptr;
   std::vector<void*> slot_ptr;  // device pointer per slot
   std::vector<void*> owned;
+  // After ipus_session_capture: the package's launches as one HIP graph.
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
 };
 
 extern "C" int ipus_session_create(ipus_context* ctx, const ipus_package* pkg, ipus_session** out) {
@@ -1100,6 +1103,8 @@ extern "C" int ipus_session_create(ipus_context* ctx, const ipus_package* pkg, i
 extern "C" int ipus_session_destroy(ipus_session* s) {
   if (!s) return 0;
   ipus_stream_sync(s->ctx);
+  if (s->exec) (void)hipGraphExecDestroy(s->exec);
+  if (s->graph) (void)hipGraphDestroy(s->graph);
   for (void* p : s->owned) ipus_buffer_free(s->ctx, p);
   delete s;
   return 0;
@@ -1150,8 +1155,9 @@ extern "C" int ipus_session_tensor_pointer(ipus_session* s, const char* name, vo
   return 0;
 }
 
-extern "C" int ipus_session_run(ipus_session* s) {
-  if (!s) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null session");
+namespace {
+// Enqueues every step of the package on the context stream.
+int launch_steps(ipus_session* s) {
   std::vector<const void*> ins;
   for (const Step& st : s->pkg->steps) {
     ins.clear();
@@ -1161,5 +1167,40 @@ extern "C" int ipus_session_run(ipus_session* s) {
                             st.scalars.data(), (int)st.scalars.size()))
       return e;
   }
+  return 0;
+}
+}  // namespace
+
+extern "C" int ipus_session_run(ipus_session* s) {
+  if (!s) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null session");
+  if (s->exec) {
+    const hipError_t e = hipGraphLaunch(s->exec, s->ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipGraphLaunch");
+  }
+  return launch_steps(s);
+}
+
+extern "C" int ipus_session_capture(ipus_session* s) {
+  if (!s) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null session");
+  if (s->exec || s->pkg->steps.empty()) return 0;
+  hipStream_t stream = s->ctx->stream;
+  hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+  const int status = launch_steps(s);
+  hipGraph_t graph = nullptr;
+  e = hipStreamEndCapture(stream, &graph);  // always ends the capture
+  if (status != 0) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return status;
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  s->graph = graph;
+  s->exec = exec;
   return 0;
 }

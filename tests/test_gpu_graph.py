@@ -161,3 +161,48 @@ def test_repeat_package_matches_unrolled_oracle(ipus, oracle, ctx):
         prod = oracle.gemm_f16(cur, w, 64, 64, 64).reshape(64, 64)
         cur = oracle.f32_to_f16(oracle.f16_to_f32(cur) + oracle.f16_to_f32(prod)).reshape(64, 64)
     assert max_rel(oracle.f16_to_f32(y), oracle.f16_to_f32(cur)) <= FP16_TOL
+
+
+def _mlp_graph(ipus, m, d, h):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [m, d])
+    w1 = g.parameter("w1", [d, h])
+    w2 = g.parameter("w2", [h, d])
+    g.set_outputs([g.gemm(g.gelu(g.gemm(x, w1)), w2)])
+    return g, {"x": (m * d, 1.0), "w1": (d * h, 0.05), "w2": (h * d, 0.05)}
+
+
+def _memory_graph(ipus, n):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [n, n])
+    t = g.transpose(x)
+    bm = g.rearrange(t, ipus.ORDER_BLOCK_MAJOR, 64, 64)
+    g.set_outputs([t, bm, g.reduce_rows(bm)])
+    return g, {"x": (n * n, 1.0)}
+
+
+@pytest.mark.parametrize("which", ["mlp", "memory"])
+def test_captured_session_replays_match_eager(ipus, ctx, which):
+    # A captured session replays its HIP graph on each run; every replay,
+    # with fresh inputs written and an eager session run in between, must
+    # equal the eager session bit for bit.
+    g, feeds = _mlp_graph(ipus, 256, 256, 512) if which == "mlp" else _memory_graph(ipus, 512)
+    pkg = ipus.build_package(g)
+    eager, graph = pkg.session(ctx), pkg.session(ctx)
+    graph.capture()
+    graph.capture()  # second call is a no-op
+    try:
+        for replay in range(4):
+            for i, (name, (count, scale)) in enumerate(feeds.items()):
+                a = synth(ipus, count, 40 + replay, i + 1, scale=scale)
+                eager.write(name, a)
+                graph.write(name, a)
+            eager.run_sync()
+            graph.run_sync()
+            eager.run_sync()  # eager work between replays
+            for t in pkg.outputs:
+                want, got = eager.read(t.name), graph.read(t.name)
+                assert np.array_equal(want.view(np.uint8), got.view(np.uint8)), (replay, t.name)
+    finally:
+        eager.close()
+        graph.close()
