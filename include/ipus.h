@@ -120,6 +120,11 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        causal, output_f16.  Shape fields follow AttentionKernelShape
  *        (kernel.rs:121-129); semantics device/flash_attention_online_f16.cpp:
  *        68-143 plus the causal limit of crates/ipu-tests/src/diagnostic.rs:741-745.
+ *   ipu_stack_flash_attention_heads_f16  as above, then query_heads,
+ *        key_heads, value_heads: operand stream s is head s % h of matrix
+ *        s / h of an unsplit [streams / h, rows, h * width] tensor (h = 1:
+ *        contiguous; streams % h == 0).  The zero-copy form of SplitHeads
+ *        (operator.rs:213-279) feeding attention; build_package emits it.
  *   ipu_stack_gelu_tanh_approx_f16     out f16; input f16; element_count
  *        (kernel.rs:1251-1263; count must be even, kernel.rs:1400-1413).
  *   ipu_stack_reduce_sum_f16           out f16; initial, packed remotes f16;

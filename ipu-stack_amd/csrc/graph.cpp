@@ -895,6 +895,61 @@ void fuse_gemm_gelu(ipus_package& pkg) {
   pkg.steps = std::move(steps);
 }
 
+bool is_attention(const std::string& symbol) {
+  return symbol == "ipu_stack_flash_attention_online_f16" ||
+         symbol == "ipu_stack_flash_attention_heads_f16";
+}
+
+// A SplitHeads (operator.rs:213-279) whose fp16 result is read only as a
+// Q, K or V operand of attention launches becomes a strided view: the
+// attention reads head s % h of the unsplit [batch, rows, h * width]
+// tensor directly (ipu_stack_flash_attention_heads_f16), and the copy and
+// its buffer disappear.
+void elide_split_heads(ipus_package& pkg) {
+  std::vector<int> writes(pkg.slots.size(), 0), reads(pkg.slots.size(), 0);
+  std::vector<bool> other_reader(pkg.slots.size(), false);
+  for (const Step& s : pkg.steps) {
+    ++writes[(size_t)s.out.slot];
+    for (const Operand& o : s.ins) {
+      ++reads[(size_t)o.slot];
+      if (!is_attention(s.symbol) || o.byte_offset != 0) other_reader[(size_t)o.slot] = true;
+    }
+  }
+  std::map<int, std::pair<Operand, uint32_t>> view;  // split result -> (unsplit operand, heads)
+  std::vector<Step> steps;
+  for (const Step& s : pkg.steps) {
+    // split_heads scalars: batch, rows, heads, head width, element bytes
+    if (s.symbol == "ipu_stack_split_heads" && s.out.byte_offset == 0 && s.scalars.size() == 5 &&
+        s.scalars[4] == 2) {
+      const size_t o = (size_t)s.out.slot;
+      if (!pkg.slots[o].external && writes[o] == 1 && reads[o] > 0 && !other_reader[o]) {
+        view[s.out.slot] = {s.ins[0], s.scalars[2]};
+        continue;
+      }
+    }
+    steps.push_back(s);
+  }
+  for (Step& s : steps) {
+    if (!is_attention(s.symbol)) continue;
+    uint32_t heads[3] = {1, 1, 1};
+    if (s.symbol == "ipu_stack_flash_attention_heads_f16")
+      for (int k = 0; k < 3; ++k) heads[k] = s.scalars[8 + (size_t)k];
+    bool changed = false;
+    for (int k = 0; k < 3; ++k) {
+      auto it = view.find(s.ins[(size_t)k].slot);
+      if (it == view.end()) continue;
+      s.ins[(size_t)k] = it->second.first;
+      heads[k] = it->second.second;
+      changed = true;
+    }
+    if (!changed) continue;
+    s.symbol = "ipu_stack_flash_attention_heads_f16";
+    s.scalars.resize(8);
+    s.scalars.insert(s.scalars.end(), heads, heads + 3);
+  }
+  pkg.steps = std::move(steps);
+}
+
 // Lifetime-packed arena offsets for non-external slots.
 uint64_t place(ipus_package& pkg) {
   for (size_t i = 0; i < pkg.steps.size(); ++i) {
@@ -981,6 +1036,7 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
   // Precision map (CompiledPackage::precisions) over every value bound to a slot.
   for (const auto& kv : b.env) pkg->precisions[kv.first] = pkg->slots[(size_t)kv.second].storage.precision;
   fuse_gemm_gelu(*pkg);
+  elide_split_heads(*pkg);
   pkg->arena_bytes = place(*pkg);
   *out = pkg.release();
   return 0;

@@ -97,14 +97,16 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds,
 // Byte offsets within a key block of the chunks this thread's DMA
 // instructions fetch: instruction i of thread t fills LDS slot i * 256 + t,
 // so it loads the chunk that the swizzle places there.
+// row_bytes is the global row pitch: D * 2 for a contiguous [streams, rows,
+// D] tensor, heads * D * 2 for a head of an unsplit [batch, rows, heads * D].
 template <int D, bool IsK>
-__device__ __forceinline__ void kv_offsets(uint32_t* voff) {
+__device__ __forceinline__ void kv_offsets(uint32_t* voff, uint32_t row_bytes) {
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) {
     const uint32_t slot = i * kThreads + threadIdx.x;
     const uint32_t row = slot / KvTile<D>::kChunks, phys = slot % KvTile<D>::kChunks;
     const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
-    voff[i] = row * KvTile<D>::kRowBytes + chunk * 16;
+    voff[i] = row * row_bytes + chunk * 16;
   }
 }
 
@@ -112,14 +114,14 @@ template <int D>
 __device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t k_rsrc,
                                          __amdgpu_buffer_rsrc_t v_rsrc, uint8_t* lk, uint8_t* lv,
                                          const uint32_t* k_voff, const uint32_t* v_voff,
-                                         uint32_t block_bytes) {
+                                         uint32_t k_block_bytes, uint32_t v_block_bytes) {
   const uint32_t wave = threadIdx.x / kWave;
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
-    dma16(k_rsrc, lk + (i * kThreads + wave * kWave) * 16, k_voff[i] + block_bytes);
+    dma16(k_rsrc, lk + (i * kThreads + wave * kWave) * 16, k_voff[i] + k_block_bytes);
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
-    dma16(v_rsrc, lv + (i * kThreads + wave * kWave) * 16, v_voff[i] + block_bytes);
+    dma16(v_rsrc, lv + (i * kThreads + wave * kWave) * 16, v_voff[i] + v_block_bytes);
 }
 
 // K fragment (first operand of S^T = K Q^T): lane holds
@@ -155,7 +157,7 @@ template <int D, bool Causal, bool OutF16>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
-    float scale_log2) {
+    float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
   constexpr uint32_t kDT = D / 32;  // output d tiles
   constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
   constexpr uint32_t kTile = KvTile<D>::kBytes;
@@ -176,17 +178,20 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const uint32_t wq0 = q0 + wave * kQueriesPerWave;  // first query of this wave
 
-  const uint16_t* Q = query + (uint64_t)stream * query_rows * D;
-  const uint16_t* K = key + (uint64_t)stream * key_rows * D;
-  const uint16_t* V = value + (uint64_t)stream * key_rows * D;
-  const int stream_bytes = (int)(key_rows * (uint32_t)D * 2u);
-  const __amdgpu_buffer_rsrc_t k_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)K, 0, stream_bytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t v_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)V, 0, stream_bytes, kBufferFlags);
+  // Stream s of an operand with h heads is head s % h of matrix s / h of a
+  // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
+  const uint32_t q_pitch = q_heads * D;
+  const uint32_t k_row_bytes = k_heads * D * 2u, v_row_bytes = v_heads * D * 2u;
+  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * D;
+  const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_heads * D + (stream % k_heads) * D;
+  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * D + (stream % v_heads) * D;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + D * 2u), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + D * 2u), kBufferFlags);
   uint32_t k_voff[KvTile<D>::kDma], v_voff[KvTile<D>::kDma];
-  kv_offsets<D, true>(k_voff);
-  kv_offsets<D, false>(v_voff);
+  kv_offsets<D, true>(k_voff, k_row_bytes);
+  kv_offsets<D, false>(v_voff, v_row_bytes);
 
   uint32_t key_end = key_rows;
   if (Causal) {
@@ -194,8 +199,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     key_end = last_q < key_rows ? last_q : key_rows;  // keys <= last query
   }
   const uint32_t nblocks = (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
-  constexpr uint32_t kBlockBytes = kKeysPerBlock * D * 2;
-  issue_kv<D>(k_rsrc, v_rsrc, lds_k0, lds_v0, k_voff, v_voff, 0);
+  const uint32_t k_block_bytes = kKeysPerBlock * k_row_bytes;
+  const uint32_t v_block_bytes = kKeysPerBlock * v_row_bytes;
+  issue_kv<D>(k_rsrc, v_rsrc, lds_k0, lds_v0, k_voff, v_voff, 0, 0);
 
   // Q fragments (second MFMA operand): lane holds Q[q][16 ks + 8 (lane/32) ..+7].
   half8_t qf[kKS];
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     q = q < query_rows ? q : query_rows - 1;
 #pragma unroll
     for (uint32_t ks = 0; ks < kKS; ++ks)
-      qf[ks] = __builtin_bit_cast(half8_t, load16(Q + (uint64_t)q * D + ks * 16 + (lane / 32) * 8));
+      qf[ks] = __builtin_bit_cast(half8_t, load16(Q + (uint64_t)q * q_pitch + ks * 16 + (lane / 32) * 8));
   }
 
   float16_t o[kDT];
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     // read: the DMA stays unconditional, which keeps the compiler's wait
     // counting exact (no vmcnt wait before the reads of this stage).
     const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
-    issue_kv<D>(k_rsrc, v_rsrc, nk, nv, k_voff, v_voff, next * kBlockBytes);
+    issue_kv<D>(k_rsrc, v_rsrc, nk, nv, k_voff, v_voff, next * k_block_bytes, next * v_block_bytes);
     const uint32_t kb = kbi * kKeysPerBlock;
     if (Causal && kb > wq0 + kQueriesPerWave - 1) return;
     const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
@@ -333,14 +339,19 @@ constexpr uint32_t kGeneralMaxValuePerLane = 8;  // value width <= 512
 __global__ __launch_bounds__(64) void attention_general_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t query_rows, uint32_t key_rows, uint32_t width,
-    uint32_t value_width, float scale_log2, bool causal, bool out_f16) {
+    uint32_t value_width, float scale_log2, bool causal, bool out_f16, uint32_t q_heads,
+    uint32_t k_heads, uint32_t v_heads) {
   const uint64_t flat = blockIdx.x;
   const uint32_t stream = (uint32_t)(flat / query_rows);
   const uint32_t row = (uint32_t)(flat % query_rows);
   const uint32_t lane = threadIdx.x;
-  const uint16_t* q = query + flat * width;
-  const uint16_t* K = key + (uint64_t)stream * key_rows * width;
-  const uint16_t* V = value + (uint64_t)stream * key_rows * value_width;
+  // Head layout as in the fast kernel; K and V rows are k_pitch / v_pitch apart.
+  const uint16_t* q = query + (((uint64_t)(stream / q_heads) * query_rows + row) * q_heads +
+                               stream % q_heads) * width;
+  const uint64_t k_pitch = (uint64_t)k_heads * width, v_pitch = (uint64_t)v_heads * value_width;
+  const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_pitch + (stream % k_heads) * width;
+  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_pitch +
+                      (stream % v_heads) * value_width;
   uint32_t allowed = key_rows;
   if (causal) allowed = row + 1 < key_rows ? row + 1 : key_rows;
   float acc[kGeneralMaxValuePerLane];
@@ -351,7 +362,7 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
     float dot = 0.0f;
     for (uint32_t d = lane; d < width; d += 64)
       dot += (float)__builtin_bit_cast(half_t, q[d]) *
-             (float)__builtin_bit_cast(half_t, K[(uint64_t)j * width + d]);
+             (float)__builtin_bit_cast(half_t, K[(uint64_t)j * k_pitch + d]);
     dot = wave_sum(dot) * scale_log2;
     const float m_new = fmaxf(m, dot);
     const float alpha = exp2f(m - m_new);
@@ -360,7 +371,7 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
 #pragma unroll
     for (uint32_t i = 0; i < kGeneralMaxValuePerLane; ++i) {
       const uint32_t c = lane + 64 * i;
-      const float v = c < value_width ? (float)__builtin_bit_cast(half_t, V[(uint64_t)j * value_width + c]) : 0.0f;
+      const float v = c < value_width ? (float)__builtin_bit_cast(half_t, V[(uint64_t)j * v_pitch + c]) : 0.0f;
       acc[i] = acc[i] * alpha + p * v;
     }
     m = m_new;
@@ -387,7 +398,7 @@ int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
                      (const uint16_t*)a.key, (const uint16_t*)a.value, a.streams, a.query_rows,
-                     a.key_rows, scale_log2);
+                     a.key_rows, scale_log2, a.heads[0], a.heads[1], a.heads[2]);
   return hip_status(hipGetLastError());
 }
 
@@ -409,9 +420,12 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   const float scale_log2 = a.scale * kLog2e;
   const bool aligned = ((uintptr_t)a.query % 16 == 0) && ((uintptr_t)a.key % 16 == 0) &&
                        ((uintptr_t)a.value % 16 == 0) && ((uintptr_t)a.out % 16 == 0);
+  for (int i = 0; i < 3; ++i)
+    if (a.heads[i] == 0 || a.streams % a.heads[i] != 0) return IPUS_ERROR_INVALID_ARGUMENT;
   // The fast kernel addresses one stream's K or V through a buffer
   // descriptor with a 31-bit byte range.
-  const bool fits = (uint64_t)a.key_rows * a.width * 2 <= 0x7fff0000ull;
+  const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
+  const bool fits = ((uint64_t)a.key_rows - 1) * kv_pitch + (uint64_t)a.width * 2 <= 0x7fff0000ull;
   if (aligned && fits && a.width == a.value_width && (a.width == 128 || a.width == 64)) {
     return a.width == 128 ? dispatch_fast<128>(stream, a, scale_log2)
                           : dispatch_fast<64>(stream, a, scale_log2);
@@ -422,7 +436,7 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   hipLaunchKernelGGL(attention_general_kernel, dim3((uint32_t)blocks), dim3(64), 0, stream, a.out,
                      (const uint16_t*)a.query, (const uint16_t*)a.key, (const uint16_t*)a.value,
                      a.query_rows, a.key_rows, a.width, a.value_width, scale_log2, a.causal,
-                     a.output_f16);
+                     a.output_f16, a.heads[0], a.heads[1], a.heads[2]);
   return hip_status(hipGetLastError());
 }
 

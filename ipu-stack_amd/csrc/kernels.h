@@ -30,6 +30,9 @@ struct AttentionArgs {
   float scale;
   bool causal;
   bool output_f16;  // false: fp32 output (reference), true: fp16
+  // Per operand (query, key, value): stream s is head s % h of matrix s / h
+  // of a [streams / h, rows, h * width] tensor; 1 = contiguous streams.
+  uint32_t heads[3] = {1, 1, 1};
 };
 
 // Dense products (k_gemm_f16.hip, k_gemm_f32.hip).

@@ -283,6 +283,29 @@ int run_gemm(ipus_context* ctx, void* out, const void* const* in, const uint32_t
   return f16 ? launch_gemm_f16(ctx->stream, a) : launch_gemm_f32(ctx->stream, a);
 }
 
+// Attention launch from the registry scalars; `heads` (query, key, value) is
+// null for the contiguous symbol.
+int run_attention(ipus_context* c, void* o, const void* const* i, const uint32_t* s,
+                  const uint32_t* heads) {
+  AttentionArgs a;
+  a.out = o;
+  a.query = i[0];
+  a.key = i[1];
+  a.value = i[2];
+  a.streams = s[0];
+  a.query_rows = s[1];
+  a.key_rows = s[2];
+  a.width = s[3];
+  a.value_width = s[4];
+  a.scale = s[5] == 0 ? 1.0f / std::sqrt((float)s[3]) : bits_to_float(s[5]);
+  a.causal = s[6] != 0;
+  a.output_f16 = s[7] != 0;
+  if (s[6] > 1 || s[7] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+  if (heads)
+    for (int k = 0; k < 3; ++k) a.heads[k] = heads[k];
+  return launch_attention_f16(c->stream, a);
+}
+
 const std::vector<KernelEntry>& registry() {
   static const std::vector<KernelEntry> entries = {
       {"ipu_stack_gemm_f16", 2,
@@ -310,21 +333,13 @@ const std::vector<KernelEntry>& registry() {
        {"matrices", "query_rows", "key_rows", "query_dimension", "value_dimension", "scale_bits",
         "causal", "output_f16"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         AttentionArgs a;
-         a.out = o;
-         a.query = i[0];
-         a.key = i[1];
-         a.value = i[2];
-         a.streams = s[0];
-         a.query_rows = s[1];
-         a.key_rows = s[2];
-         a.width = s[3];
-         a.value_width = s[4];
-         a.scale = s[5] == 0 ? 1.0f / std::sqrt((float)s[3]) : bits_to_float(s[5]);
-         a.causal = s[6] != 0;
-         a.output_f16 = s[7] != 0;
-         if (s[6] > 1 || s[7] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
-         return launch_attention_f16(c->stream, a);
+         return run_attention(c, o, i, s, nullptr);
+       }},
+      {"ipu_stack_flash_attention_heads_f16", 3,
+       {"matrices", "query_rows", "key_rows", "query_dimension", "value_dimension", "scale_bits",
+        "causal", "output_f16", "query_heads", "key_heads", "value_heads"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return run_attention(c, o, i, s, s + 8);
        }},
       {"ipu_stack_gelu_tanh_approx_f16", 1, {"element_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {

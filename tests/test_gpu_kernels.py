@@ -356,6 +356,36 @@ def test_attention_causal_first_row_is_first_value(ipus, oracle, ctx):
     assert np.allclose(got[:, 0, :], vf[:, 0, :], rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("batch,heads,s,d", [(2, 2, 256, 128), (1, 4, 200, 64), (2, 3, 40, 72)])
+def test_attention_heads_view_equals_split_copy(ipus, oracle, ctx, causal, batch, heads, s, d):
+    """The strided-heads launch on unsplit [batch, rows, heads * d] operands is
+    bit-identical to the contiguous launch on split_heads copies (the split is
+    a pure permutation, operator.rs:213-279).  K stays pre-split (1 head) to
+    cover mixed layouts."""
+    streams = batch * heads
+    qx = synth(ipus, batch * s * heads * d, 61, 1, 1).reshape(batch, s, heads * d)
+    kx = synth(ipus, batch * s * heads * d, 61, 2, 1).reshape(batch, s, heads * d)
+    vx = synth(ipus, batch * s * heads * d, 61, 3, 1).reshape(batch, s, heads * d)
+    qs, ks, vs = (oracle.f32_to_f16(oracle.split_heads(oracle.f16_to_f32(t), heads))
+                  for t in (qx, kx, vx))
+    common = [streams, s, s, d, d, 0, int(causal), 0]
+    want = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * d * 4, [qs, ks, vs],
+               common, np.float32)
+    got = run(ctx, "ipu_stack_flash_attention_heads_f16", streams * s * d * 4, [qx, ks, vx],
+              common + [heads, 1, heads], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_attention_heads_view_rejects_uneven_heads(ipus, ctx):
+    buf = ctx.alloc(1 << 16)
+    with pytest.raises(ipus.IpusError) as e:  # 3 streams are not whole 2-head matrices
+        ctx.launch("ipu_stack_flash_attention_heads_f16", buf, [buf, buf, buf],
+                   [3, 4, 4, 16, 16, 0, 0, 0, 2, 1, 1])
+    assert e.value.status == ipus.ERROR_INVALID_ARGUMENT
+    buf.free()
+
+
 @pytest.mark.parametrize("causal,s", [(True, 4096), (False, 2048)])
 def test_attention_baseline_size_sampled_rows(ipus, oracle, ctx, causal, s):
     """BASELINE config 5 at full size (B8*H16 = 128 streams, D = 128), 256 query

@@ -180,6 +180,48 @@ def test_gemm_gelu_fusion_needs_a_private_result(ipus):
     assert "ipu_stack_gemm_f16_gelu" not in steps
 
 
+def _projected_attention(ipus, b=2, s=128, d=256, heads=2):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [b, s, d])
+    proj = [g.gemm(x, g.parameter(n, [d, d])) for n in ("wq", "wk", "wv")]
+    q, k, v = (g.split_heads(p, heads) for p in proj)
+    return g, proj, (q, k, v)
+
+
+def test_split_heads_feeding_attention_is_a_strided_view(ipus):
+    # graph.rs:338-362 structure: the three head splits become the heads
+    # layout of one attention launch, and their buffers leave the arena.
+    g, proj, (q, k, v) = _projected_attention(ipus)
+    g.set_outputs([g.flash_attention_with_options(q, k, v, causal=True)])
+    pkg = ipus.build_package(g)
+    syms = [s[0] for s in pkg.steps]
+    assert "ipu_stack_split_heads" not in syms
+    assert syms[-1] == "ipu_stack_flash_attention_heads_f16"
+    assert pkg.steps[-1][2][8:] == (2, 2, 2)  # query, key, value heads
+    assert pkg.steps[-1][2][:5] == (4, 128, 128, 128, 128)
+    # only the three projections (2 * 128 * 256 fp16 each) are in the arena
+    assert pkg.arena_bytes == 3 * 2 * 128 * 256 * 2
+
+
+def test_split_heads_with_another_reader_is_copied(ipus):
+    # The split K is also a graph output: its copy stays and only Q and V
+    # are read through the view.
+    g, proj, (q, k, v) = _projected_attention(ipus)
+    g.set_outputs([g.flash_attention_with_options(q, k, v, causal=False), k])
+    pkg = ipus.build_package(g)
+    syms = [s[0] for s in pkg.steps]
+    assert syms.count("ipu_stack_split_heads") == 1
+    att = [s for s in pkg.steps if s[0].startswith("ipu_stack_flash_attention")]
+    assert att[0][0] == "ipu_stack_flash_attention_heads_f16" and att[0][2][8:] == (2, 1, 2)
+    # fp32 compute: the split result is cast before attention, no view
+    g, proj, (q, k, v) = _projected_attention(ipus)
+    g.set_outputs([g.flash_attention_with_options(q, k, v, causal=False)])
+    pkg = ipus.build_package(g, ipus.PackageConfig(compute_precision="f32"))
+    syms = [s[0] for s in pkg.steps]
+    assert syms.count("ipu_stack_split_heads") == 3
+    assert "ipu_stack_flash_attention_online_f16" in syms
+
+
 def test_build_package_arena_reuses_dead_values(ipus):
     g = ipus.ComputeGraph()
     x = g.host_input("x", [1024, 1024])
