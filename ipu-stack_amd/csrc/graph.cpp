@@ -101,12 +101,6 @@ int graph_error(const std::string& message) {
   return fail(IPUS_ERROR_GRAPH, "%s", message.c_str());
 }
 
-std::string shape_str(const Shape& s) {
-  std::string r = "[";
-  for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
-  return r + "]";
-}
-
 // graph.rs:755-777
 bool broadcast(const Shape& left, const Shape& right, Shape* out, std::string* error) {
   const size_t rank = std::max(left.size(), right.size());

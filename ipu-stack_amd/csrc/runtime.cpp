@@ -37,6 +37,12 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(IPUS_ERROR_HIP_BASE - (int)e, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// Makes the context's device current for the calling thread.
+int use_device(const ipus_context* ctx) {
+  const hipError_t e = hipSetDevice(ctx->device);
+  return e == hipSuccess ? 0 : hip_fail(e, "hipSetDevice");
+}
+
 int check_launch(int status, const char* symbol) {
   if (status == 0) return 0;
   if (status <= IPUS_ERROR_HIP_BASE)
@@ -104,11 +110,15 @@ extern "C" int ipus_context_create(int device, ipus_context** out) {
 
 extern "C" int ipus_context_destroy(ipus_context* ctx) {
   if (!ctx) return 0;
-  hipSetDevice(ctx->device);
-  hipStreamSynchronize(ctx->stream);
-  hipStreamDestroy(ctx->stream);
+  // The context is released even when the device reports an error; the
+  // first error is returned.
+  int status = use_device(ctx);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess && status == 0) status = hip_fail(e, "hipStreamSynchronize");
+  e = hipStreamDestroy(ctx->stream);
+  if (e != hipSuccess && status == 0) status = hip_fail(e, "hipStreamDestroy");
   delete ctx;
-  return 0;
+  return status;
 }
 
 extern "C" int ipus_context_device_info(ipus_context* ctx, ipus_device_info* info) {
@@ -139,7 +149,7 @@ extern "C" int ipus_context_stream(ipus_context* ctx, void** stream) {
 // ---------------------------------------------------------------------------
 extern "C" int ipus_buffer_alloc(ipus_context* ctx, size_t bytes, void** ptr) {
   if (!ctx || !ptr) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
-  hipSetDevice(ctx->device);
+  if (int e = use_device(ctx)) return e;
   // 256-byte aligned by hipMalloc; zero-byte requests get a valid pointer.
   hipError_t e = hipMalloc(ptr, bytes ? bytes : 256);
   if (e == hipErrorOutOfMemory)
@@ -151,7 +161,7 @@ extern "C" int ipus_buffer_alloc(ipus_context* ctx, size_t bytes, void** ptr) {
 extern "C" int ipus_buffer_free(ipus_context* ctx, void* ptr) {
   if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
   if (!ptr) return 0;
-  hipSetDevice(ctx->device);
+  if (int e = use_device(ctx)) return e;
   hipError_t e = hipFree(ptr);
   if (e != hipSuccess) return hip_fail(e, "hipFree");
   return 0;
@@ -210,7 +220,7 @@ extern "C" int ipus_stream_sync(ipus_context* ctx) {
 
 extern "C" int ipus_event_create(ipus_context* ctx, ipus_event** out) {
   if (!ctx || !out) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
-  hipSetDevice(ctx->device);
+  if (int e = use_device(ctx)) return e;
   auto* ev = new ipus_event();
   hipError_t e = hipEventCreate(&ev->event);
   if (e != hipSuccess) {
@@ -223,9 +233,9 @@ extern "C" int ipus_event_create(ipus_context* ctx, ipus_event** out) {
 
 extern "C" int ipus_event_destroy(ipus_event* ev) {
   if (!ev) return 0;
-  hipEventDestroy(ev->event);
+  const hipError_t e = hipEventDestroy(ev->event);
   delete ev;
-  return 0;
+  return e == hipSuccess ? 0 : hip_fail(e, "hipEventDestroy");
 }
 
 extern "C" int ipus_event_record(ipus_context* ctx, ipus_event* ev) {
@@ -557,7 +567,7 @@ extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
     if (!inputs || !inputs[k])
       return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null input %d", symbol, k);
   if (scalar_count && !scalars) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null scalars");
-  hipSetDevice(ctx->device);
+  if (int e = use_device(ctx)) return e;
   return check_launch(e->launch(ctx, output, inputs, scalars), symbol);
 }
 
