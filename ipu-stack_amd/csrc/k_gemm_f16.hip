@@ -22,11 +22,15 @@
 //   * both swizzles are free of bank conflicts for 32 banks x 4 bytes and for
 //     64 banks x 4 bytes (the XOR patterns below are checked for both);
 //   * two LDS stages, each a distinct LDS object; BK = 64 is four 16-k
-//     substeps whose fragments are double-buffered in registers.  All reads
-//     of a stage are issued during its first three substeps, so the one
-//     raw s_barrier per K step sits before the fourth: that substep's MFMAs
-//     cover the DMA for step + 2 (into the stage just released) and the
-//     first fragment reads of step + 1;
+//     substeps.  Fragments are read two substeps ahead into four register
+//     buffers, so every read of a stage is issued by the end of its step's
+//     second substep and the one raw s_barrier per K step sits before the
+//     third: substeps 2-3 issue the DMA for step + 2 (into the stage just
+//     released) and the first two substeps' reads of step + 1.  Reading two
+//     substeps ahead absorbs the delay that the DMA's LDS writes add to the
+//     fragment reads (a scratch build without those writes ran 32% faster);
+//   * fragment addresses are one lane base per operand with the substep and
+//     block folded in as XOR / immediate offsets (equal to kc_off / mc_off);
 //   * the MFMA computes the tile of C^T (B fragment as the first operand) so
 //     each lane holds 4 consecutive columns of one row of C (one 8-byte store);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
@@ -110,27 +114,6 @@ __device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, uint8_t*
 #pragma unroll
   for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j)
     dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024, voff[j], soffset);
-}
-
-// Fragment for v_mfma_f32_32x32x16_f16: lane holds X[row0 + lane % 32][16 ks +
-// 8 (lane / 32) .. +7] of the operand whose rows are `row0 ..` (m for A, n for B).
-template <int BK, bool KContig>
-__device__ __forceinline__ half8_t read_frag(const uint8_t* tile, uint32_t row0, uint32_t ks,
-                                             uint32_t lane) {
-  if constexpr (KContig) {
-    return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(
-                                           tile + kc_off<BK>(row0 + lane % 32, ks * 2 + lane / 32)));
-  } else {
-    const uint32_t group = lane / 16, s = lane % 16;
-    const uint32_t mn = row0 + (group % 2) * 16 + 4 * (s % 4);
-    const uint32_t k = ks * 16 + (group / 2) * 8 + s / 4;
-    const uint32_t byte_in_chunk = (mn % 8) * 2;
-    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (LDS_AS short4_t*)(tile + mc_off(k, mn / 8) + byte_in_chunk));
-    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (LDS_AS short4_t*)(tile + mc_off(k + 4, mn / 8) + byte_in_chunk));
-    return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-  }
 }
 
 // fp16 result of one accumulator; with Gelu, GELU of that fp16 value (the
@@ -220,58 +203,91 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   fetch(lds_a0, lds_b0, 0);
   fetch(lds_a1, lds_b1, clamp(1));
 
-  // 4 substeps of 16 k.  Substep s multiplies buffer
-  // s % 2 while the fragments of substep s + 1 are read; every read of the
-  // current stage is issued during substeps 0..2, so the per-step barrier
-  // sits before substep 3, whose MFMAs then cover the DMA of step kt + 2
-  // (into the stage just released) and the reads of step kt + 1's first
-  // substep.
-  half8_t fa[2][4], fb[2][4];
-  constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
-  auto read_sub = [&](const uint8_t* ta, const uint8_t* tb, uint32_t ks, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[buf][i] = read_frag<BK, kAK>(ta, wm + 32 * i, ks, lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) fb[buf][j] = read_frag<BK, kBK_>(tb, wn + 32 * j, ks, lane);
+  // Fragment addresses from per-lane bases (equal to kc_off / mc_off):
+  // K-contiguous rows w0 + 32 i + lane % 32, chunk 2 ks + lane / 32:
+  //   (kbase ^ ((2 ks ^ 4 (i & 1)) << 4)) + 4096 i;
+  // MN-contiguous transposed reads for column block j, substep ks, high half:
+  //   (mbase ^ 64 j) + 8192 ks + 2048 hi.
+  auto k_base = [&](uint32_t w0) {
+    const uint32_t b = lane / 32, s0 = (lane & 7) ^ ((lane % 32) / 8);
+    return (w0 + lane % 32) * 128 + ((b ^ s0) << 4);
   };
-  auto mma = [&](int buf) {
+  auto m_base = [&](uint32_t w0) {
+    const uint32_t group = lane / 16, s = lane % 16, t = s / 4;
+    const uint32_t sw = (t << 1) ^ (t << 2), c_l = 2 * (group % 2) + (s % 4) / 2;
+    const uint32_t mn0 = w0 + (group % 2) * 16 + 4 * (s % 4);
+    return ((group / 2) * 8 + t) * 512 + (w0 / 8) * 16 + 16 * (c_l ^ (sw & 3)) + (mn0 % 8) * 2 +
+           64 * ((sw >> 2) & 3);
+  };
+  const uint32_t a_base_l = kAK ? k_base(wm) : m_base(wm);
+  const uint32_t b_base_l = kBK_ ? k_base(wn) : m_base(wn);
+  auto frag = [&]<bool KContig>(const uint8_t* tile, uint32_t base, int blk, int ks) __attribute__((always_inline)) {
+    if constexpr (KContig) {
+      return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(
+                                             tile + ((base ^ (((2 * ks) ^ (4 * (blk & 1))) << 4)) + 4096 * blk)));
+    } else {
+      const uint32_t a = (base ^ (64 * blk)) + 8192 * ks;
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a));
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a + 2048));
+      return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+
+  // Four fragment buffers: substep s multiplies buffer s and its reads fill
+  // buffer (s + 2) % 4, two substeps ahead.  Every read of a stage is then
+  // issued by the end of its step's substep 1, so the per-step barrier sits
+  // before substep 2; the DMA of step kt + 2 goes into the stage just
+  // released during substeps 2-3 and has four substeps to land.
+  half8_t fa[4][4], fb[4][4];
+  constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
+  auto read_sub = [&](const uint8_t* ta, const uint8_t* tb, int ks, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[buf][i] = frag.template operator()<kAK>(ta, a_base_l, i, ks);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[buf][j] = frag.template operator()<kBK_>(tb, b_base_l, j, ks);
+  };
+  auto mma = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
   };
+  auto sched = [&](int dma) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (m < dma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   read_sub(lds_a0, lds_b0, 0, 0);
-  auto step = [&](uint8_t* ta, uint8_t* tb, const uint8_t* na, const uint8_t* nb, uint32_t kt) {
+  read_sub(lds_a0, lds_b0, 1, 1);
+  auto step = [&](uint8_t* ta, uint8_t* tb, const uint8_t* na, const uint8_t* nb, uint32_t kt)
+      __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      read_sub(ta, tb, s + 1, (s + 1) % 2);
-      mma(s % 2);
-    }
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-    }
+    read_sub(ta, tb, 2, 2);
+    mma(0);
+    sched(0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_sub(ta, tb, 3, 3);
+    mma(1);
+    sched(0);
     __builtin_amdgcn_sched_barrier(0);
     // This wave's reads of (ta, tb) have returned and its DMA of step kt + 1
     // has landed; after the barrier, every wave's have.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    fetch(ta, tb, clamp(kt + 2));
+    issue_tile<BK>(a_rsrc, ta, wave, a_voff, clamp(kt + 2) * a_kstep);
     read_sub(na, nb, 0, 0);
-    mma(1);
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (m < 2 * kDma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    mma(2);
+    sched(kDma);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_tile<BK>(b_rsrc, tb, wave, b_voff, clamp(kt + 2) * b_kstep);
+    read_sub(na, nb, 1, 1);
+    mma(3);
+    sched(kDma);
   };
 
   uint32_t kt = 0;
