@@ -131,6 +131,14 @@ __global__ __launch_bounds__(kThreads) void block_major_f16_kernel(
 // (its 256 / cb column blocks are consecutive): the register-transposed 8x8
 // blocks are placed in LDS at their offsets in that run, and the run is then
 // written with whole-line streaming stores.
+// LDS slot of 16-byte chunk p of the staged run: XOR-swizzled so that the
+// transposed 8x8 blocks a 16-lane group stores (8 column chunks x 2 row
+// halves) hit distinct bank groups for column blocks 16 and 64 (unswizzled:
+// 8-way conflicts), while the sequential read-back stays conflict-free.
+__device__ __forceinline__ uint32_t stage_chunk(uint32_t p) {
+  return p ^ ((((p >> 4) ^ (p >> 6)) & 7u) << 1);
+}
+
 __global__ __launch_bounds__(kThreads) void block_major64_f16_kernel(
     uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t columns,
     uint32_t column_block, uint32_t tiles_c) {
@@ -153,14 +161,14 @@ __global__ __launch_bounds__(kThreads) void block_major64_f16_kernel(
   for (int i = 0; i < 8; ++i) {
     const uint32_t c = cl + i;
     const uint32_t off = ((c / cb) * 4 + rl / 16) * 16 * cb + (c % cb) * 16 + rl % 16;
-    *reinterpret_cast<u32x4*>(stage + off * 2) = out[i];
+    *reinterpret_cast<u32x4*>(stage + stage_chunk(off / 8) * 16) = out[i];
   }
   __syncthreads();
   uint16_t* run = d + (uint64_t)tr * columns * 64 + (uint64_t)tc * 16384;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t v = k * kThreads + threadIdx.x;
-    store16_nt(run + v * 8, *reinterpret_cast<const u32x4*>(stage + v * 16));
+    store16_nt(run + v * 8, *reinterpret_cast<const u32x4*>(stage + stage_chunk(v) * 16));
   }
 }
 
