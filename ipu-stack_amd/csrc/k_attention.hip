@@ -15,6 +15,10 @@
 //     are copied global -> LDS with buffer_load ... lds (16 bytes per lane, no
 //     staging registers; rows past the end of the stream read as 0), both
 //     stored row-major [64 keys][D] with an XOR swizzle of 16-byte chunks;
+//   * software pipeline: step j runs ONE MFMA cluster holding the scores of
+//     block j and the output update of block j - 1 (alternating, fragments
+//     read ahead, the step's DMA instructions spread between them), then the
+//     softmax of block j on the VALU.  K tiles run one block ahead of V;
 //   * scores are computed transposed, S^T = K Q^T, with
 //     v_mfma_f32_32x32x16_f16 (K fragments by ds_read_b128 as the first
 //     operand, Q fragments resident in registers as the second), so a lane
@@ -28,7 +32,8 @@
 //   * the running max moves only when a block's max exceeds it by more than
 //     kRescaleSlack (log2 units): the result is exact for any reference
 //     point, probabilities stay <= 2^kRescaleSlack, and most blocks skip the
-//     rescale of the output accumulators;
+//     rescale of the output accumulators and the exchange of the max with
+//     the partner lane;
 //   * causal: key blocks past the workgroup's last query are never loaded, a
 //     wave skips blocks past its own last query.
 //   * workgroups are remapped so each XCD (round-robin dispatch over 8) runs
@@ -94,63 +99,19 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)lds, 16, voffset, 0, 0, 0);
 }
 
-// Byte offsets within a key block of the chunks this thread's DMA
-// instructions fetch: instruction i of thread t fills LDS slot i * 256 + t,
-// so it loads the chunk that the swizzle places there.
-// row_bytes is the global row pitch: D * 2 for a contiguous [streams, rows,
-// D] tensor, heads * D * 2 for a head of an unsplit [batch, rows, heads * D].
+// Byte offset within a key block of the chunk this thread's first DMA
+// instruction fetches: instruction i of thread t fills LDS slot i * 256 + t,
+// so it loads the chunk that the swizzle places there.  Instruction i covers
+// the rows kThreads / kChunks * i further on with the same swizzled chunk (the
+// swizzles depend only on row bits that this step leaves alone), so the other
+// instructions add a wave-uniform row offset.  row_bytes is the global row
+// pitch: D * 2 for a contiguous [streams, rows, D] tensor, heads * D * 2 for a
+// head of an unsplit [batch, rows, heads * D].
 template <int D, bool IsK>
-__device__ __forceinline__ void kv_offsets(uint32_t* voff, uint32_t row_bytes) {
-#pragma unroll
-  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) {
-    const uint32_t slot = i * kThreads + threadIdx.x;
-    const uint32_t row = slot / KvTile<D>::kChunks, phys = slot % KvTile<D>::kChunks;
-    const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
-    voff[i] = row * row_bytes + chunk * 16;
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void issue_kv(__amdgpu_buffer_rsrc_t k_rsrc,
-                                         __amdgpu_buffer_rsrc_t v_rsrc, uint8_t* lk, uint8_t* lv,
-                                         const uint32_t* k_voff, const uint32_t* v_voff,
-                                         uint32_t k_block_bytes, uint32_t v_block_bytes) {
-  const uint32_t wave = threadIdx.x / kWave;
-#pragma unroll
-  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
-    dma16(k_rsrc, lk + (i * kThreads + wave * kWave) * 16, k_voff[i] + k_block_bytes);
-#pragma unroll
-  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
-    dma16(v_rsrc, lv + (i * kThreads + wave * kWave) * 16, v_voff[i] + v_block_bytes);
-}
-
-// K fragment (first operand of S^T = K Q^T): lane holds
-// K[32 st + lane % 32][16 ks + 8 (lane / 32) .. +7].
-template <int D>
-__device__ __forceinline__ half8_t k_frag(const uint8_t* lk, uint32_t st, uint32_t ks,
-                                          uint32_t lane) {
-  return __builtin_bit_cast(
-      half8_t, *reinterpret_cast<const u32x4*>(lk + k_off<D>(st * 32 + lane % 32, ks * 2 + lane / 32)));
-}
-
-// V^T fragment (first operand of O^T += V^T P^T) for d tile dt and the 16
-// keys 32 st + 16 h + {0..15}: lane holds d = 32 dt + lane % 32 and, in
-// element e, key 32 st + 16 h + 8 (e / 4) + 4 (lane / 32) + e % 4, the key
-// order of score accumulator elements 8 h .. 8 h + 7.  Each transposed read
-// returns 4 consecutive keys: in a 16-lane group, source lane s addresses row
-// key0 + s / 4, columns d0 + 4 (s % 4) .. +3.
-template <int D>
-__device__ __forceinline__ half8_t v_frag(const uint8_t* lv, uint32_t st, uint32_t h, uint32_t dt,
-                                          uint32_t lane) {
-  const uint32_t s = lane % 16, g = lane / 32, dg = (lane / 16) % 2;
-  const uint32_t key = 32 * st + 16 * h + 4 * g + s / 4;
-  const uint32_t d = 32 * dt + 16 * dg + 4 * (s % 4);
-  const uint32_t byte = (d % 8) * 2;
-  const short4_t lo =
-      __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(lv + v_off<D>(key, d / 8) + byte));
-  const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (LDS_AS short4_t*)(lv + v_off<D>(key + 8, d / 8) + byte));
-  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+__device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes) {
+  const uint32_t row = threadIdx.x / KvTile<D>::kChunks, phys = threadIdx.x % KvTile<D>::kChunks;
+  const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
+  return row * row_bytes + chunk * 16;
 }
 
 template <int D, bool Causal, bool OutF16>
@@ -161,6 +122,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   constexpr uint32_t kDT = D / 32;  // output d tiles
   constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
   constexpr uint32_t kTile = KvTile<D>::kBytes;
+  constexpr uint32_t kDmaRows = kThreads / KvTile<D>::kChunks;  // rows per DMA instruction
+  static_assert(4 * kDT == 2 * kKS, "one PV MFMA per score MFMA");
   // Two stages, each a distinct LDS object so the compiler can see that the
   // DMA into one stage never aliases the fragment reads of the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTile];
@@ -175,8 +138,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   const uint32_t stream = pid / qblocks;
   const uint32_t qb = Causal ? qblocks - 1 - pid % qblocks : pid % qblocks;
   const uint32_t q0 = qb * kQueriesPerBlock;
-  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t wq0 = q0 + wave * kQueriesPerWave;  // first query of this wave
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+  const uint32_t wq0 = q0 + wave_s * kQueriesPerWave;  // first query of this wave
 
   // Stream s of an operand with h heads is head s % h of matrix s / h of a
   // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
@@ -189,9 +153,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
       (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + D * 2u), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + D * 2u), kBufferFlags);
-  uint32_t k_voff[KvTile<D>::kDma], v_voff[KvTile<D>::kDma];
-  kv_offsets<D, true>(k_voff, k_row_bytes);
-  kv_offsets<D, false>(v_voff, v_row_bytes);
+  const uint32_t k_voff = kv_offset<D, true>(k_row_bytes), v_voff = kv_offset<D, false>(v_row_bytes);
 
   uint32_t key_end = key_rows;
   if (Causal) {
@@ -201,7 +163,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   const uint32_t nblocks = (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
   const uint32_t k_block_bytes = kKeysPerBlock * k_row_bytes;
   const uint32_t v_block_bytes = kKeysPerBlock * v_row_bytes;
-  issue_kv<D>(k_rsrc, v_rsrc, lds_k0, lds_v0, k_voff, v_voff, 0, 0);
+  // Blocks this wave computes scores for (causal: keys <= its last query).
+  // Every such block holds at least one allowed key per query of the wave.
+  uint32_t nproc = nblocks;
+  if (Causal) {
+    const uint32_t lim = (wq0 + kQueriesPerWave - 1) / kKeysPerBlock + 1;
+    nproc = lim < nproc ? lim : nproc;
+  }
 
   // Q fragments (second MFMA operand): lane holds Q[q][16 ks + 8 (lane/32) ..+7].
   half8_t qf[kKS];
@@ -220,38 +188,134 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float m_run = -INFINITY;  // reference point, log2 units (scaled)
   float l_run = 0.0f;       // this lane's share of the row sum
+  half8_t pp[2][2];         // fp16 probabilities of the last softmax
   const uint32_t qi = wq0 + lane % 32;
 
-  auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi) {
-    // This wave's DMA of block kbi has landed (vmcnt(0)); after the barrier
-    // every wave's has, and every wave is done reading the other stage.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // The last block re-fetches itself into the stage that is no longer
-    // read: the DMA stays unconditional, which keeps the compiler's wait
-    // counting exact (no vmcnt wait before the reads of this stage).
-    const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
-    issue_kv<D>(k_rsrc, v_rsrc, nk, nv, k_voff, v_voff, next * k_block_bytes, next * v_block_bytes);
-    const uint32_t kb = kbi * kKeysPerBlock;
-    if (Causal && kb > wq0 + kQueriesPerWave - 1) return;
-    const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
+  // Fragment reads.  K fragment (first operand of S^T = K Q^T): lane holds
+  // K[32 st + lane % 32][16 ks + 8 (lane / 32) .. +7].  V^T fragment (first
+  // operand of O^T += V^T P^T) for d tile dt and keys 32 st + 16 h + {0..15}:
+  // lane holds d = 32 dt + lane % 32 and, in element e, key 32 st + 16 h +
+  // 8 (e / 4) + 4 (lane / 32) + e % 4, the key order of score accumulator
+  // elements 8 h .. 8 h + 7; each ds_read_b64_tr_b16 returns 4 consecutive
+  // keys (in a 16-lane group, source lane s addresses row key0 + s / 4,
+  // columns d0 + 4 (s % 4) .. +3).  Offsets are those of the first rows
+  // XORed with the k step (chunk 2 ks: bits 5..) or d tile (chunk 4 dt: bits
+  // 6..), since both swizzles XOR the chunk with row bits; other rows add a
+  // constant.  kb_step / vb_step are reloaded opaquely each step so the XORs
+  // stay in the loop instead of taking one register per offset.
+  const uint32_t kbase = k_off<D>(lane % 32, lane / 32);
+  uint32_t vbase;
+  {
+    const uint32_t sl = lane % 16, g = lane / 32, dg = (lane / 16) % 2;
+    const uint32_t d = 16 * dg + 4 * (sl % 4);
+    vbase = v_off<D>(4 * g + sl / 4, d / 8) + (d % 8) * 2;
+  }
+  uint32_t kb_step = kbase, vb_step = vbase;
+  auto kfrag = [&](const uint8_t* lk, uint32_t st, uint32_t ks) __attribute__((always_inline)) {
+    const uint8_t* p = lk + (kb_step ^ (ks << 5)) + st * 32 * KvTile<D>::kRowBytes;
+    return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(p));
+  };
+  auto vfrag = [&](const uint8_t* lv, uint32_t st, uint32_t h, uint32_t dt) __attribute__((always_inline)) {
+    const uint8_t* p = lv + (vb_step ^ (dt << 6)) + (32 * st + 16 * h) * KvTile<D>::kRowBytes;
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
+    const short4_t hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 8 * KvTile<D>::kRowBytes));
+    return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
 
-    // S^T for 64 keys x 32 queries: s[st][r] is key kb + 32 st + 8 (r/4) +
-    // 4 (lane/32) + r%4 of query qi.
-    float16_t s[2];
+  // DMA instruction i of a K or V tile.  The scalar part is opaque so the
+  // per-instruction offsets are not hoisted out of the loop into registers;
+  // the block offset stays in the vector offset, which the range check of
+  // the buffer descriptor covers (rows past the end read as 0).
+  auto dma_k = [&](uint32_t i, uint8_t* nk, uint32_t bytes) __attribute__((always_inline)) {
+    uint32_t so = bytes + i * kDmaRows * k_row_bytes;
+    asm volatile("" : "+s"(so));
+    dma16(k_rsrc, nk + (i * kThreads + wave_s * kWave) * 16, k_voff + so);
+  };
+  auto dma_v = [&](uint32_t i, uint8_t* nv, uint32_t bytes) __attribute__((always_inline)) {
+    uint32_t so = bytes + i * kDmaRows * v_row_bytes;
+    asm volatile("" : "+s"(so));
+    dma16(v_rsrc, nv + (i * kThreads + wave_s * kWave) * 16, v_voff + so);
+  };
+
+  // Software pipeline over key blocks: step j runs one MFMA cluster with the
+  // scores of block j and the output update of block j - 1 (from pp), with
+  // the step's DMA spread over it, then the softmax of block j on the VALU.
+  // K tiles run one block ahead of V tiles: step j fetches K(j + 1) and V(j),
+  // each into the stage last read in step j - 1.
+  auto cluster = [&]<bool WithPv>(float16_t* s, const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
+                                   uint8_t* nv, uint32_t kbi) __attribute__((always_inline)) {
+    const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
+    // K fragments two k steps ahead, V fragments one.
+    constexpr uint32_t kAhead = 2;
+    half8_t kf[kAhead][2], vf[2];
+#pragma unroll
+    for (uint32_t ks = 0; ks < kAhead; ++ks)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) kf[ks][st] = kfrag(lk, st, ks);
+    if constexpr (WithPv) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) vf[st] = vfrag(lv, 0, 0, st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // Raised priority while this wave feeds the matrix pipe: the other wave
     // on the SIMD fills the gaps with its softmax.
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (uint32_t ks = 0; ks < kKS; ++ks)
+    for (uint32_t ks = 0; ks < kKS; ++ks) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
-        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k_frag<D>(lk, st, ks, lane), qf[ks], s[st], 0, 0, 0);
+      for (int st = 0; st < 2; ++st) {
+        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks % kAhead][st], qf[ks], s[st], 0, 0, 0);
+        if constexpr (WithPv) {
+          // PV MFMA n = 2 ks + st of 16: (st, h) pair n / kDT, d tile n % kDT.
+          const uint32_t n = 2 * ks + st, c = n / kDT, dt = n % kDT;
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[st], pp[c / 2][c % 2], o[dt], 0, 0, 0);
+        }
+      }
+      if (ks + kAhead < kKS) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) kf[ks % kAhead][st] = kfrag(lk, st, ks + kAhead);
+      }
+      if constexpr (WithPv) {
+        if (ks + 1 < kKS) {
+#pragma unroll
+          for (int st = 0; st < 2; ++st) {
+            const uint32_t n = 2 * (ks + 1) + st, c = n / kDT, dt = n % kDT;
+            vf[st] = vfrag(lv, c / 2, c % 2, dt);
+          }
+        }
+      }
+      // DMA instructions spread over the k steps: K tile first, then V.
+      constexpr uint32_t kDmaPer = (2 * KvTile<D>::kDma + kKS - 1) / kKS;
+#pragma unroll
+      for (uint32_t u = 0; u < kDmaPer; ++u) {
+        const uint32_t i = ks * kDmaPer + u;
+        if (i < KvTile<D>::kDma) dma_k(i, nk, next * k_block_bytes);
+        else if (i < 2 * KvTile<D>::kDma) dma_v(i - KvTile<D>::kDma, nv, kbi * v_block_bytes);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     __builtin_amdgcn_s_setprio(0);
-
+  };
+  // Output update of the previous block alone (V tile lv).
+  auto pv_only = [&](const uint8_t* lv) __attribute__((always_inline)) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (uint32_t dt = 0; dt < kDT; ++dt)
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vfrag(lv, st, h, dt), pp[st][h], o[dt], 0, 0, 0);
+  };
+  // Softmax of block kbi.  s[st][r] is the score of key kb + 32 st + 8 (r/4)
+  // + 4 (lane/32) + r%4 for query qi; the result goes to pp.
+  auto softmax = [&](float16_t* s, uint32_t kbi) __attribute__((always_inline)) {
+    const uint32_t kb = kbi * kKeysPerBlock;
+    const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
     if (need_mask) {
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -261,15 +325,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
           if ((Causal && kj > qi) || kj >= key_rows) s[st][r] = -INFINITY;
         }
     }
+    // Max over this lane's 32 keys.  The partner lane (lane ^ 32: the other
+    // 32 keys of the same query) is consulted only when some lane's max
+    // passes the slack, so both halves always share one reference point;
+    // the max is finite (at least one allowed key per query).
     float mx = s[0][0];
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-    mx = max_with_partner(mx) * scale_log2;
-    // Every processed block holds at least one allowed key per query, so mx
-    // is finite; the reference point moves only by more than the slack.
+    mx *= scale_log2;
     if (__any(mx > m_run + kRescaleSlack)) {
+      mx = max_with_partner(mx);
       const float m_new = mx > m_run + kRescaleSlack ? mx : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
@@ -288,25 +355,55 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           pf[e] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
-        // The row sum adds the fp16 probabilities that the MFMA consumes, in
-        // fp32 (v_dot2 with ones: exact products, fp32 accumulation).
-#pragma unroll
-        for (int e = 0; e < 8; e += 2)
-          l_run = __builtin_amdgcn_fdot2(half2_t{pf[e], pf[e + 1]}, half2_t{1, 1}, l_run, false);
-#pragma unroll
-        for (uint32_t dt = 0; dt < kDT; ++dt)
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_frag<D>(lv, st, h, dt, lane), pf, o[dt], 0, 0, 0);
+        // The row sum adds the fp16 probabilities that the MFMA consumes:
+        // pairs, then quads, in fp16 (each p <= 2^kRescaleSlack, so a quad
+        // sum stays far inside the fp16 range and carries at most two
+        // roundings), then fp32 accumulation with v_dot2.
+        const half2_t s01 = half2_t{pf[0], pf[1]} + half2_t{pf[2], pf[3]};
+        const half2_t s45 = half2_t{pf[4], pf[5]} + half2_t{pf[6], pf[7]};
+        l_run = __builtin_amdgcn_fdot2(s01 + s45, half2_t{1, 1}, l_run, false);
+        pp[st][h] = pf;
       }
   };
 
-  uint32_t kbi = 0;
-  for (; kbi + 1 < nblocks; kbi += 2) {
-    step(lds_k0, lds_v0, lds_k1, lds_v1, kbi);
-    step(lds_k1, lds_v1, lds_k0, lds_v0, kbi + 1);
+  auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi)
+      __attribute__((always_inline)) {
+    // Every wave's DMA of K(kbi) and V(kbi - 1) has landed, and every wave
+    // is done reading K(kbi - 1) and V(kbi - 2), whose stages the DMA of this
+    // step overwrites.  The last block re-fetches its K tile: the DMA stays
+    // unconditional, which keeps the compiler's wait counting exact.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    kb_step = kbase;
+    vb_step = vbase;
+    asm volatile("" : "+v"(kb_step), "+v"(vb_step));
+    float16_t s[2];
+    if (kbi > 0 && kbi < nproc) {
+      cluster.template operator()<true>(s, lk, lv, nk, nv, kbi);
+      softmax(s, kbi);
+    } else if (kbi == 0) {
+      cluster.template operator()<false>(s, lk, lv, nk, nv, kbi);
+      softmax(s, kbi);
+    } else {
+      // Past this wave's last block: the DMA, and the pending output update.
+      const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
+#pragma unroll
+      for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, nk, next * k_block_bytes);
+#pragma unroll
+      for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_v(i, nv, kbi * v_block_bytes);
+      if (kbi == nproc) pv_only(lv);
+    }
+  };
+
+  // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j).
+#pragma unroll
+  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, lds_k0, 0);
+  for (uint32_t kbi = 0; kbi < nblocks; kbi += 2) {
+    step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
+    if (kbi + 1 < nblocks) step(lds_k1, lds_v0, lds_k0, lds_v1, kbi + 1);
   }
-  if (kbi < nblocks) step(lds_k0, lds_v0, lds_k1, lds_v1, kbi);
-  // Drain the last (redundant) DMA before the workgroup can exit.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // V of the last block (and every DMA) has landed after this barrier.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
   // o[dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][qi], unnormalised.
   const float l_total = sum_with_partner(l_run);
