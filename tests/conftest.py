@@ -45,3 +45,17 @@ def max_rel(got, want) -> float:
     want = np.asarray(want, dtype=np.float64)
     denom = float(np.max(np.abs(want))) if want.size else 1.0
     return float(np.max(np.abs(got - want))) / (denom if denom > 0 else 1.0) if want.size else 0.0
+
+
+def ref_style_ok(got, want, atol=0.03, rtol=0.03) -> bool:
+    """The reference's per-element check |y - r| <= atol + rtol |r| with its
+    default atol = rtol = 0.03 (crates/ipu-tests/src/main.rs:47-53)."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return bool(np.all(np.abs(got - want) <= atol + rtol * np.abs(want)))
+
+
+def fp16_close(got, want, tol=1e-2) -> bool:
+    """fp16 parity: normwise max-rel <= tol (the gating metric) and the
+    reference's own per-element tolerance."""
+    return max_rel(got, want) <= tol and ref_style_ok(got, want)

@@ -13,7 +13,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import max_rel
+from conftest import fp16_close, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -50,7 +50,7 @@ def test_mlp_package_matches_oracle_and_fusion_is_exact(ipus, oracle, ctx):
     assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16"]
     hidden = oracle.gelu_f16(oracle.gemm_f16(xs, w1s, m, h, d)).reshape(m, h)
     want = oracle.f16_to_f32(oracle.gemm_f16(hidden, w2s, m, d, h)).reshape(m, d)
-    assert max_rel(oracle.f16_to_f32(y), want) <= FP16_TOL
+    assert fp16_close(oracle.f16_to_f32(y), want, FP16_TOL)
     # The fused launch equals GEMM then GELU bit for bit.
     bx, b1 = ctx.upload(xs), ctx.upload(w1s)
     fused, plain, act = ctx.alloc(m * h * 2), ctx.alloc(m * h * 2), ctx.alloc(m * h * 2)
@@ -100,7 +100,7 @@ def test_attention_package_matches_oracle(ipus, oracle, ctx):
             .reshape(b, s, d) for n in ws}
     qh, kh, vh = (oracle.split_heads(proj[n], heads) for n in ("wq", "wk", "wv"))
     want = oracle.attention(qh, kh, vh, b * heads, s, s, d // heads, d // heads, causal=True)
-    assert max_rel(o.reshape(-1, d // heads), want) <= FP16_TOL
+    assert fp16_close(o.reshape(-1, d // heads), want, FP16_TOL)
 
 
 def test_memory_chain_package_bit_exact(ipus, oracle, ctx):
@@ -141,7 +141,7 @@ def test_add_broadcast_and_f32_compute_package(ipus, oracle, ctx):
     _, (yh,) = run_package(ipus, ctx, g, {"x": xs, "bias": bs, "w": wsr})
     added = oracle.f32_to_f16(oracle.add_f32(xf, bf)).reshape(-1, 32)
     want16 = oracle.f16_to_f32(oracle.gemm_f16(added, wsr, 4 * 64, 48, 32)).reshape(4, 64, 48)
-    assert max_rel(oracle.f16_to_f32(yh), want16) <= FP16_TOL
+    assert fp16_close(oracle.f16_to_f32(yh), want16, FP16_TOL)
 
 
 def test_repeat_package_matches_unrolled_oracle(ipus, oracle, ctx):
@@ -160,7 +160,7 @@ def test_repeat_package_matches_unrolled_oracle(ipus, oracle, ctx):
     for w in wv:
         prod = oracle.gemm_f16(cur, w, 64, 64, 64).reshape(64, 64)
         cur = oracle.f32_to_f16(oracle.f16_to_f32(cur) + oracle.f16_to_f32(prod)).reshape(64, 64)
-    assert max_rel(oracle.f16_to_f32(y), oracle.f16_to_f32(cur)) <= FP16_TOL
+    assert fp16_close(oracle.f16_to_f32(y), oracle.f16_to_f32(cur), FP16_TOL)
 
 
 def _mlp_graph(ipus, m, d, h):

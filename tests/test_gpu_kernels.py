@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import max_rel
+from conftest import fp16_close, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -209,7 +209,7 @@ def gemm_case(ipus, oracle, ctx, M, N, K, tl=False, tr=False, batches=1, bl=True
                                    (17, 19, 72), (1, 1, 1), (300, 200, 100), (1024, 1024, 1024)])
 def test_gemm_f16_shapes(ipus, oracle, ctx, M, N, K):
     got, want = gemm_case(ipus, oracle, ctx, M, N, K)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
 
 
 @pytest.mark.parametrize("tl", [False, True])
@@ -217,13 +217,13 @@ def test_gemm_f16_shapes(ipus, oracle, ctx, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(256, 512, 128), (100, 60, 40)])
 def test_gemm_f16_transposes(ipus, oracle, ctx, tl, tr, M, N, K):
     got, want = gemm_case(ipus, oracle, ctx, M, N, K, tl, tr)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
 
 
 @pytest.mark.parametrize("bl,br", [(True, True), (True, False), (False, True)])
 def test_gemm_f16_batched_broadcast(ipus, oracle, ctx, bl, br):
     got, want = gemm_case(ipus, oracle, ctx, 256, 256, 128, batches=3, bl=bl, br=br)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
 
 
 def test_gemm_f16_one_hot_kat_bit_exact(ipus, oracle, ctx):
@@ -262,7 +262,7 @@ def test_gemm_f16_8192_sampled_rows(ipus, oracle, ctx):
     rows = np.array([i * (n - 1) // 63 for i in range(64)], dtype=np.uint32)
     want = oracle.gemm_f16_rows(a, b, n, n, n, rows)
     got_rows = oracle.f16_to_f32(got.reshape(n, n)[rows])
-    assert max_rel(got_rows, want) <= FP16_TOL
+    assert fp16_close(got_rows, want, FP16_TOL)
 
 
 # ---------------------------------------------------------------------------
@@ -322,13 +322,32 @@ def attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal, scale=None
                                              (2, 100, 37, 128), (1, 19, 17, 72)])
 def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, d, causal)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
 
 
 def test_attention_scale_and_f16_output(ipus, oracle, ctx):
     got, want = attention_case(ipus, oracle, ctx, 2, 256, 256, 128, 128, True, scale=0.05,
                                out_f16=True)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
+
+
+def test_attention_reference_smoke_tolerance(ipus, oracle, ctx):
+    """The reference's fused attention smoke (crates/ipu-tests/src/main.rs:669-671,
+    1305-1505): 4 heads x 17 queries x 19 keys x width 72, inputs ~ N(0, 0.25) in
+    fp16, non-causal, fp32 output; every element checked against an fp32 softmax
+    with max abs error <= 0.012 and rms <= 0.003.  (The reference's input
+    bitstream comes from rand_distr and is not reproduced: same distribution,
+    this build's seeded generator.)"""
+    heads, sq, sk, d = 4, 17, 19, 72
+    q = synth(ipus, heads * sq * d, 0x6174, 1, 1, 0.25)
+    k = synth(ipus, heads * sk * d, 0x6174, 2, 1, 0.25)
+    v = synth(ipus, heads * sk * d, 0x6174, 3, 1, 0.25)
+    got = run(ctx, "ipu_stack_flash_attention_online_f16", heads * sq * d * 4, [q, k, v],
+              [heads, sq, sk, d, d, 0, 0, 0], np.float32).reshape(-1, d)
+    want = oracle.attention(oracle.f16_to_f32(q), oracle.f16_to_f32(k), oracle.f16_to_f32(v),
+                            heads, sq, sk, d, d, False, None)
+    err = np.abs(got.astype(np.float64) - want)
+    assert err.max() <= 0.012 and np.sqrt(np.mean(err ** 2)) <= 0.003
 
 
 def test_attention_uniform_values_give_values(ipus, oracle, ctx):
@@ -394,7 +413,7 @@ def test_attention_baseline_size_sampled_rows(ipus, oracle, ctx, causal, s):
     total = streams * s
     rows = [i * (total - 1) // 255 for i in range(256)]
     got, want = attention_case(ipus, oracle, ctx, streams, s, s, d, d, causal, rows=rows, seed=55)
-    assert max_rel(got, want) <= FP16_TOL
+    assert fp16_close(got, want, FP16_TOL)
 
 
 # ---------------------------------------------------------------------------
