@@ -428,3 +428,42 @@ def test_launch_pointer_arity(ipus, ctx):
         ctx.launch("ipu_stack_no_such_kernel", buf, [], [])
     assert e.value.status == ipus.ERROR_UNKNOWN_SYMBOL
     buf.free()
+
+
+def test_empty_launches_touch_nothing(ipus, ctx):
+    """Launches with an empty extent succeed and leave the output untouched."""
+    sentinel = np.full(64, 0x3C00, dtype=np.uint16)
+    buf = ctx.upload(sentinel)
+    src = ctx.upload(np.zeros(64, dtype=np.uint16))
+    cases = [
+        ("ipu_stack_gemm_f16", [src, src], [1, 0, 8, 8, 0, 0, 0, 0]),
+        ("ipu_stack_gemm_f16", [src, src], [0, 8, 8, 8, 0, 0, 0, 0]),
+        ("ipu_stack_gemm_f32", [src, src], [1, 8, 0, 8, 0, 0, 0, 0]),
+        ("ipu_stack_flash_attention_online_f16", [src, src, src], [0, 16, 16, 64, 64, 0, 1, 0]),
+        ("ipu_stack_flash_attention_online_f16", [src, src, src], [2, 0, 16, 64, 64, 0, 0, 0]),
+        ("ipu_stack_gelu_tanh_approx_f16", [src], [0]),
+        ("ipu_stack_transpose_f16", [src], [1, 0, 8]),
+        ("ipu_stack_copy", [src], [0]),
+        ("ipu_stack_fill_zero", [], [0]),
+        ("ipu_stack_cast_f16_f32", [src], [0]),
+        ("ipu_stack_reduce_rows_f16", [src], [0, 8, 3, 0, 0]),
+    ]
+    for symbol, inputs, scalars in cases:
+        ctx.launch(symbol, buf, inputs, scalars)
+    ctx.sync()
+    assert np.array_equal(buf.download(np.uint16), sentinel)
+    for b in (buf, src):
+        b.free()
+
+
+@pytest.mark.parametrize("symbol,elem", [("ipu_stack_gemm_f16", 2), ("ipu_stack_gemm_f32", 4)])
+def test_gemm_empty_inner_dimension_is_zero(ipus, ctx, symbol, elem):
+    """K = 0: every output element is an empty sum, 0."""
+    m, n = 8, 24
+    out = ctx.upload(np.full(m * n * elem // 2, 0x3C00, dtype=np.uint16))
+    src = ctx.upload(np.zeros(64, dtype=np.uint16))
+    ctx.launch(symbol, out, [src, src], [1, m, n, 0, 0, 0, 0, 0])
+    got = out.download(np.uint16)
+    assert not np.any(got)
+    for b in (out, src):
+        b.free()
