@@ -36,8 +36,10 @@
 //     the partner lane;
 //   * causal: key blocks past the workgroup's last query are never loaded, a
 //     wave skips blocks past its own last query.
-//   * workgroups are remapped so each XCD (round-robin dispatch over 8) runs
-//     whole streams, heaviest query blocks first, sharing K and V in its L2.
+//   * causal: one workgroup runs query blocks n - 1 - i and then i of one
+//     stream, so every workgroup has the same number of key steps;
+//     workgroups are remapped so each XCD (round-robin dispatch over 8) runs
+//     whole streams, sharing K and V in its L2.
 #include "../../include/ipus.h"
 #include "device_common.h"
 #include "kernels.h"
@@ -115,10 +117,10 @@ __device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes) {
 }
 
 template <int D, bool Causal, bool OutF16>
-__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
+__device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
-    const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
-    float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
+    const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
+    uint32_t key_rows, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
   constexpr uint32_t kDT = D / 32;  // output d tiles
   constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
   constexpr uint32_t kTile = KvTile<D>::kBytes;
@@ -131,12 +133,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTile];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTile];
 
-  const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const uint32_t total = qblocks * streams;
-  uint32_t pid = blockIdx.x;
-  if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;  // XCD-contiguous
-  const uint32_t stream = pid / qblocks;
-  const uint32_t qb = Causal ? qblocks - 1 - pid % qblocks : pid % qblocks;
   const uint32_t q0 = qb * kQueriesPerBlock;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -408,25 +404,53 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   // o[dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][qi], unnormalised.
   const float l_total = sum_with_partner(l_run);
   const float inv = 1.0f / l_total;
-  if (qi >= query_rows) return;
-  const uint64_t row = ((uint64_t)stream * query_rows + qi) * D;
-#pragma unroll
-  for (uint32_t dt = 0; dt < kDT; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
-      if constexpr (OutF16) {
-        half4_t hv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][4 * g + e] * inv);
-        *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
-      } else {
-        float4_t fv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) fv[e] = o[dt][4 * g + e] * inv;
-        *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
+  if (qi < query_rows) {
+    const uint64_t row = ((uint64_t)stream * query_rows + qi) * D;
+  #pragma unroll
+    for (uint32_t dt = 0; dt < kDT; ++dt)
+  #pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
+        if constexpr (OutF16) {
+          half4_t hv;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][4 * g + e] * inv);
+          *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
+        } else {
+          float4_t fv;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) fv[e] = o[dt][4 * g + e] * inv;
+          *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
+        }
       }
-    }
+  }
+}
+
+// One workgroup per query block (non-causal), or per pair of query blocks
+// i and n - 1 - i of one stream (causal: the pair's key steps add up to the
+// same count for every workgroup).  Workgroups are remapped so each XCD
+// (round-robin dispatch over 8) runs whole streams, sharing K and V in its L2.
+template <int D, bool Causal, bool OutF16>
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
+    void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
+    const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
+    float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
+  const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  const uint32_t per_stream = Causal ? (qblocks + 1) / 2 : qblocks;
+  const uint32_t total = per_stream * streams;
+  uint32_t pid = blockIdx.x;
+  if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;  // XCD-contiguous
+  const uint32_t stream = pid / per_stream, i = pid % per_stream;
+  // Causal: the heavy block first, then its mirror (none for the middle
+  // block of an odd count).
+  const uint32_t reps = Causal && i != qblocks - 1 - i ? 2 : 1;
+  for (uint32_t rep = 0; rep < reps; ++rep) {
+    // Every wave is done with the LDS stages before the next block's DMA.
+    if (rep > 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint32_t qb = Causal ? (rep == 0 ? qblocks - 1 - i : i) : i;
+    attention_block<D, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
+                                       scale_log2, q_heads, k_heads, v_heads);
+  }
 }
 
 // General attention: one 64-lane block per (stream, query row); any widths.
@@ -490,7 +514,7 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
 template <int D, bool Causal, bool OutF16>
 int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   const uint32_t qblocks = (a.query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const uint64_t blocks = (uint64_t)qblocks * a.streams;
+  const uint64_t blocks = (uint64_t)(Causal ? (qblocks + 1) / 2 : qblocks) * a.streams;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
   hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
