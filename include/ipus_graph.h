@@ -138,7 +138,10 @@ int ipus_package_value_precision(const ipus_package *package, ipus_value value, 
 
 /* ---- session: device buffers for one package ---- */
 typedef struct ipus_session ipus_session;
+/* The session borrows context and package: both must outlive it.  One
+ * session is used from one thread at a time (HostSession's contract). */
 int ipus_session_create(ipus_context *context, const ipus_package *package, ipus_session **out);
+/* Releases the session even after a device error; returns the first error. */
 int ipus_session_destroy(ipus_session *session);
 /* Binding names: the graph input names; outputs are "output.<i>". */
 int ipus_session_write(ipus_session *session, const char *name, const void *host, size_t bytes);

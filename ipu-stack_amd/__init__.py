@@ -697,8 +697,8 @@ class Session:
 
     def close(self) -> None:
         if self.handle:
-            _lib().ipus_session_destroy(self.handle)
-            self.handle = None
+            handle, self.handle = self.handle, None
+            _check(_lib().ipus_session_destroy(handle))
 
     def __del__(self):
         try:

@@ -1152,12 +1152,22 @@ extern "C" int ipus_session_create(ipus_context* ctx, const ipus_package* pkg, i
 
 extern "C" int ipus_session_destroy(ipus_session* s) {
   if (!s) return 0;
-  ipus_stream_sync(s->ctx);
-  if (s->exec) (void)hipGraphExecDestroy(s->exec);
-  if (s->graph) (void)hipGraphDestroy(s->graph);
-  for (void* p : s->owned) ipus_buffer_free(s->ctx, p);
+  // The session is released even when the device reports an error; the
+  // first error is returned.
+  int status = use_device(s->ctx);
+  if (int e = ipus_stream_sync(s->ctx); e && !status) status = e;
+  if (s->exec) {
+    const hipError_t e = hipGraphExecDestroy(s->exec);
+    if (e != hipSuccess && !status) status = hip_fail(e, "hipGraphExecDestroy");
+  }
+  if (s->graph) {
+    const hipError_t e = hipGraphDestroy(s->graph);
+    if (e != hipSuccess && !status) status = hip_fail(e, "hipGraphDestroy");
+  }
+  for (void* p : s->owned)
+    if (int e = ipus_buffer_free(s->ctx, p); e && !status) status = e;
   delete s;
-  return 0;
+  return status;
 }
 
 namespace {

@@ -18,6 +18,8 @@ namespace ipus {
 // Records a formatted message as the thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t e, const char* what);
+// Makes the context's device current for the calling thread.
+int use_device(const ipus_context* ctx);
 // Turns a launcher status into a recorded error for `symbol`.
 int check_launch(int status, const char* symbol);
 
