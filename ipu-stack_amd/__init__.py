@@ -342,8 +342,9 @@ class DeviceBuffer:
 
     def free(self) -> None:
         if self.ptr:
-            _check(_lib().ipus_buffer_free(self.context.handle, self.ptr))
-            self.ptr = 0
+            ptr, self.ptr = self.ptr, 0
+            self.context._buffers.discard(self)
+            _check(_lib().ipus_buffer_free(self.context.handle, ptr))
 
     def download(self, dtype, shape=None) -> np.ndarray:
         dtype = np.dtype(dtype)
@@ -360,16 +361,21 @@ class Context:
         h = ctypes.c_void_p()
         _check(_lib().ipus_context_create(int(device), ctypes.byref(h)))
         self.handle = h.value
-        self._buffers: list[DeviceBuffer] = []
+        self._buffers: set[DeviceBuffer] = set()  # live buffers, freed by close()
 
     def close(self) -> None:
+        """Frees the live buffers and the context; raises the first error
+        after releasing everything."""
         if self.handle:
+            handle, self.handle = self.handle, None
+            status = 0
             for b in self._buffers:
                 if b.ptr:
-                    _lib().ipus_buffer_free(self.handle, b.ptr)
+                    status = status or _lib().ipus_buffer_free(handle, b.ptr)
                     b.ptr = 0
-            _lib().ipus_context_destroy(self.handle)
-            self.handle = None
+            self._buffers.clear()
+            status = status or _lib().ipus_context_destroy(handle)
+            _check(status)
 
     def __enter__(self):
         return self
@@ -393,7 +399,7 @@ class Context:
         p = ctypes.c_void_p()
         _check(_lib().ipus_buffer_alloc(self.handle, int(nbytes), ctypes.byref(p)))
         buf = DeviceBuffer(self, p.value, int(nbytes))
-        self._buffers.append(buf)
+        self._buffers.add(buf)
         return buf
 
     def upload(self, array: np.ndarray) -> DeviceBuffer:
