@@ -7,7 +7,8 @@
 // crates/ipu-tests/src/diagnostic.rs:711-780 (key j allowed iff j <= i when
 // causal, 741-745; scale default 1/sqrt(width), 733-736).
 //
-// Fast kernel (width == value width in {64, 128}):
+// Fast kernel (width == value width, a multiple of 8 up to 128, computed in
+// tiles 64 or 128 columns wide with zero padding):
 //   * 256 threads = 4 waves; a wave owns 32 queries, a workgroup 128 queries
 //     of one stream; two workgroups share a CU (launch bound), so one SIMD
 //     runs the softmax of one wave while the MFMA pipe serves the other;
@@ -107,20 +108,25 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds,
 // the rows kThreads / kChunks * i further on with the same swizzled chunk (the
 // swizzles depend only on row bits that this step leaves alone), so the other
 // instructions add a wave-uniform row offset.  row_bytes is the global row
-// pitch: D * 2 for a contiguous [streams, rows, D] tensor, heads * D * 2 for a
-// head of an unsplit [batch, rows, heads * D].
+// pitch: width * 2 for a contiguous [streams, rows, width] tensor, heads *
+// width * 2 for a head of an unsplit [batch, rows, heads * width].  Chunks at
+// or past the width (a width below the tile's D, padded) get an offset past
+// the buffer's range, so their loads return 0: kPadOffset plus any block
+// offset (< 2^31) stays above the range (< 0x7fff0000) without wrapping.
+constexpr uint32_t kPadOffset = 0x80000000u;
 template <int D, bool IsK>
-__device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes) {
+__device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes, uint32_t width) {
   const uint32_t row = threadIdx.x / KvTile<D>::kChunks, phys = threadIdx.x % KvTile<D>::kChunks;
   const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
-  return row * row_bytes + chunk * 16;
+  return chunk * 8 < width ? row * row_bytes + chunk * 16 : kPadOffset;
 }
 
 template <int D, bool Causal, bool OutF16>
 __device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
-    uint32_t key_rows, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
+    uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
+    uint32_t v_heads) {
   constexpr uint32_t kDT = D / 32;  // output d tiles
   constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
   constexpr uint32_t kTile = KvTile<D>::kBytes;
@@ -140,16 +146,18 @@ __device__ __forceinline__ void attention_block(
 
   // Stream s of an operand with h heads is head s % h of matrix s / h of a
   // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
-  const uint32_t q_pitch = q_heads * D;
-  const uint32_t k_row_bytes = k_heads * D * 2u, v_row_bytes = v_heads * D * 2u;
-  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * D;
-  const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_heads * D + (stream % k_heads) * D;
-  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * D + (stream % v_heads) * D;
+  // The tile width D is the stream width padded to 64 or 128.
+  const uint32_t q_pitch = q_heads * width;
+  const uint32_t k_row_bytes = k_heads * width * 2u, v_row_bytes = v_heads * width * 2u;
+  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * width;
+  const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_heads * width + (stream % k_heads) * width;
+  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * width + (stream % v_heads) * width;
   const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + D * 2u), kBufferFlags);
+      (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + width * 2u), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + D * 2u), kBufferFlags);
-  const uint32_t k_voff = kv_offset<D, true>(k_row_bytes), v_voff = kv_offset<D, false>(v_row_bytes);
+      (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + width * 2u), kBufferFlags);
+  const uint32_t k_voff = kv_offset<D, true>(k_row_bytes, width);
+  const uint32_t v_voff = kv_offset<D, false>(v_row_bytes, width);
 
   uint32_t key_end = key_rows;
   if (Causal) {
@@ -174,7 +182,11 @@ __device__ __forceinline__ void attention_block(
     q = q < query_rows ? q : query_rows - 1;
 #pragma unroll
     for (uint32_t ks = 0; ks < kKS; ++ks)
-      qf[ks] = __builtin_bit_cast(half8_t, load16(Q + (uint64_t)q * q_pitch + ks * 16 + (lane / 32) * 8));
+    {
+      const uint32_t d0 = ks * 16 + (lane / 32) * 8;  // padding columns are 0
+      qf[ks] = __builtin_bit_cast(
+          half8_t, d0 < width ? load16(Q + (uint64_t)q * q_pitch + d0) : u32x4{0, 0, 0, 0});
+    }
   }
 
   float16_t o[kDT];
@@ -405,20 +417,21 @@ __device__ __forceinline__ void attention_block(
   const float l_total = sum_with_partner(l_run);
   const float inv = 1.0f / l_total;
   if (qi < query_rows) {
-    const uint64_t row = ((uint64_t)stream * query_rows + qi) * D;
-  #pragma unroll
+    const uint64_t row = ((uint64_t)stream * query_rows + qi) * width;
+#pragma unroll
     for (uint32_t dt = 0; dt < kDT; ++dt)
-  #pragma unroll
+#pragma unroll
       for (int g = 0; g < 4; ++g) {
         const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
+        if (d >= width) continue;  // padding (width is a multiple of 8)
         if constexpr (OutF16) {
           half4_t hv;
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][4 * g + e] * inv);
           *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
         } else {
           float4_t fv;
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 4; ++e) fv[e] = o[dt][4 * g + e] * inv;
           *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
         }
@@ -434,7 +447,7 @@ template <int D, bool Causal, bool OutF16>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
-    float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
+    uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
   const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
   const uint32_t per_stream = Causal ? (qblocks + 1) / 2 : qblocks;
   const uint32_t total = per_stream * streams;
@@ -449,7 +462,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     if (rep > 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const uint32_t qb = Causal ? (rep == 0 ? qblocks - 1 - i : i) : i;
     attention_block<D, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
-                                       scale_log2, q_heads, k_heads, v_heads);
+                                       width, scale_log2, q_heads, k_heads, v_heads);
   }
 }
 
@@ -519,7 +532,7 @@ int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
                      (const uint16_t*)a.key, (const uint16_t*)a.value, a.streams, a.query_rows,
-                     a.key_rows, scale_log2, a.heads[0], a.heads[1], a.heads[2]);
+                     a.key_rows, a.width, scale_log2, a.heads[0], a.heads[1], a.heads[2]);
   return hip_status(hipGetLastError());
 }
 
@@ -544,12 +557,15 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   for (int i = 0; i < 3; ++i)
     if (a.heads[i] == 0 || a.streams % a.heads[i] != 0) return IPUS_ERROR_INVALID_ARGUMENT;
   // The fast kernel addresses one stream's K or V through a buffer
-  // descriptor with a 31-bit byte range.
+  // descriptor with a 31-bit byte range; the offsets of the last block's
+  // rows (up to 63 past the end) and of padding chunks stay below 2^32.
   const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
-  const bool fits = ((uint64_t)a.key_rows - 1) * kv_pitch + (uint64_t)a.width * 2 <= 0x7fff0000ull;
-  if (aligned && fits && a.width == a.value_width && (a.width == 128 || a.width == 64)) {
-    return a.width == 128 ? dispatch_fast<128>(stream, a, scale_log2)
-                          : dispatch_fast<64>(stream, a, scale_log2);
+  const bool fits = ((uint64_t)a.key_rows + kKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
+  // Widths that are multiples of 8 up to 128 run in 64- or 128-wide tiles
+  // (zero padding); others take the general kernel.
+  if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 128) {
+    return a.width > 64 ? dispatch_fast<128>(stream, a, scale_log2)
+                        : dispatch_fast<64>(stream, a, scale_log2);
   }
   if (a.value_width > 64 * kGeneralMaxValuePerLane) return IPUS_ERROR_UNAVAILABLE;
   const uint64_t blocks = (uint64_t)a.streams * a.query_rows;

@@ -319,7 +319,9 @@ def attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal, scale=None
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("streams,sq,sk,d", [(2, 256, 256, 128), (3, 300, 300, 128),
                                              (1, 512, 512, 64), (4, 64, 64, 128),
-                                             (2, 100, 37, 128), (1, 19, 17, 72)])
+                                             (2, 100, 37, 128), (1, 19, 17, 72),
+                                             (2, 130, 130, 96), (1, 70, 90, 40),
+                                             (2, 64, 64, 8), (1, 256, 200, 120)])
 def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, d, causal)
     assert fp16_close(got, want, FP16_TOL)
@@ -376,7 +378,8 @@ def test_attention_causal_first_row_is_first_value(ipus, oracle, ctx):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("batch,heads,s,d", [(2, 2, 256, 128), (1, 4, 200, 64), (2, 3, 40, 72)])
+@pytest.mark.parametrize("batch,heads,s,d", [(2, 2, 256, 128), (1, 4, 200, 64), (2, 3, 40, 72),
+                                             (1, 16, 130, 72)])
 def test_attention_heads_view_equals_split_copy(ipus, oracle, ctx, causal, batch, heads, s, d):
     """The strided-heads launch on unsplit [batch, rows, heads * d] operands is
     bit-identical to the contiguous launch on split_heads copies (the split is
