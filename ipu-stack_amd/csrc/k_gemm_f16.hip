@@ -5,7 +5,8 @@
 // evaluator's fp32 sgemm followed by one fp16 rounding
 // (crates/ipu-tests/src/diagnostic.rs:533-654, 841-847).
 //
-// Fast kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0):
+// Fast kernel (16-byte aligned operands; N and K multiples of 8, and M too
+// when A is transposed; any M, N, K otherwise):
 //   * block tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each
 //     wave owns 128 x 128 of C as 4 x 4 tiles of v_mfma_f32_32x32x16_f16;
 //   * operand tiles go global -> LDS with buffer_load ... lds (16 bytes per
@@ -36,7 +37,13 @@
 //     stages each wave's 128 x 128 result in LDS and writes 256-byte row
 //     runs with streaming stores (8192^3: +4%; 4096 x 16384 x 4096: +17%);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
-//     dispatch over 8 XCDs) form a compact group of C tiles sharing L2.
+//     dispatch over 8 XCDs) form a compact group of C tiles sharing L2;
+//   * partial tiles: rows of a K-contiguous operand past M or N, and rows of
+//     an MN-contiguous one past K, lie past the buffer's range and read as
+//     0; MN-contiguous chunks past M or N, and (in the KTail instantiation,
+//     K % 64 != 0) K-contiguous chunks past K on the last step, get an
+//     offset past the range; the epilogue stores only rows < M and 8-column
+//     chunks < N.
 // General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
 #include "../../include/ipus.h"
 #include "device_common.h"
@@ -88,9 +95,15 @@ struct Tile {
 // offset) of the DMA instructions this wave issues for one operand tile.  The
 // DMA writes lane i at base + 16 i, so each lane fetches the global chunk
 // that the swizzle places at its LDS slot.
+// Offset of a chunk outside the operand (past M or N along an MN-contiguous
+// row, or past K on the last K step of a K-contiguous row): beyond every
+// buffer range (< 2^31) plus any K offset (< 2^31) without wrapping, so the
+// load returns 0.
+constexpr uint32_t kPadOffset = 0x80000000u;
+
 template <int BK, bool KContig>
 __device__ __forceinline__ void tile_offsets(uint32_t wave, uint32_t lane, uint32_t ld,
-                                             uint32_t* voff) {
+                                             uint32_t mn_limit, uint32_t* voff) {
   constexpr int kChunks = BK / 8;  // 16-byte chunks per K-contiguous row
 #pragma unroll
   for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
@@ -105,7 +118,9 @@ __device__ __forceinline__ void tile_offsets(uint32_t wave, uint32_t lane, uint3
       const uint32_t k = inst * 2 + lane / 32;  // 2 rows of 512 bytes
       const uint32_t phys = lane % 32;
       const uint32_t chunk = (mc_off(k, phys) - k * 512u) >> 4;
-      voff[j] = (k * ld + chunk * 8) * 2;
+      // mn_limit: columns of this tile inside the operand (rows past K are
+      // past the buffer's range already).
+      voff[j] = chunk * 8 < mn_limit ? (k * ld + chunk * 8) * 2 : kPadOffset;
     }
   }
 }
@@ -118,6 +133,22 @@ __device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, uint8_t*
     dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024, voff[j], soffset);
 }
 
+// The last K step of a K-contiguous operand when K % BK != 0: chunks whose
+// k range starts at or past k_limit (the step's valid k count) read 0.
+template <int BK>
+__device__ __forceinline__ void issue_tile_k_tail(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
+                                                  uint32_t wave, uint32_t lane, const uint32_t* voff,
+                                                  uint32_t soffset, uint32_t k_limit) {
+  constexpr int kChunks = BK / 8;
+#pragma unroll
+  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
+    const uint32_t row = (wave * Tile<BK>::kDmaPerWave + j) * (1024 / (BK * 2)) + lane / kChunks;
+    const uint32_t chunk = (kc_off<BK>(row, lane % kChunks) - row * (BK * 2)) >> 4;
+    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024,
+          chunk * 8 < k_limit ? voff[j] : kPadOffset, soffset);
+  }
+}
+
 // fp16 result of one accumulator; with Gelu, GELU of that fp16 value (the
 // same number the separate GELU kernel would produce from the stored GEMM
 // output).
@@ -128,7 +159,7 @@ __device__ __forceinline__ half_t epilogue(float acc) {
   return h;
 }
 
-template <bool TransposeLeft, bool TransposeRight, bool Gelu>
+template <bool TransposeLeft, bool TransposeRight, bool Gelu, bool KTail>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
@@ -145,7 +176,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   constexpr bool kAK = !TransposeLeft;  // A rows (m) K-contiguous
   constexpr bool kBK_ = TransposeRight; // B^T rows (n) K-contiguous
 
-  const uint32_t nbm = M / kBM, nbn = N / kBN;
+  const uint32_t nbm = (M + kBM - 1) / kBM, nbn = (N + kBN - 1) / kBN;
   const uint32_t tiles = nbm * nbn;
   uint32_t pid = blockIdx.x;
   if (tiles % 8 == 0) pid = (pid % 8) * (tiles / 8) + pid / 8;  // XCD-contiguous
@@ -178,8 +209,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = threadIdx.x % kWave;
   uint32_t a_voff[kDma], b_voff[kDma];
-  tile_offsets<BK, kAK>(wave, lane, kAK ? K : M, a_voff);
-  tile_offsets<BK, kBK_>(wave, lane, kBK_ ? K : N, b_voff);
+  tile_offsets<BK, kAK>(wave, lane, kAK ? K : M, M - m0, a_voff);
+  tile_offsets<BK, kBK_>(wave, lane, kBK_ ? K : N, N - n0, b_voff);
   // K advance per step in bytes.
   const uint32_t a_kstep = kAK ? BK * 2 : BK * M * 2;
   const uint32_t b_kstep = kBK_ ? BK * 2 : BK * N * 2;
@@ -194,11 +225,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const uint32_t ksteps = K / BK;
+  const uint32_t ksteps = (K + BK - 1) / BK;
+  // K-contiguous operands mask the chunks past K on the last step (MN-
+  // contiguous rows past K are past the buffer's range).
+  const uint32_t k_tail = K % BK;
   auto clamp = [&](uint32_t k) { return k < ksteps ? k : ksteps - 1; };
+  // KTail (K % BK != 0) is a separate instantiation, so the branch never
+  // enters the scheduled K loop of the common case.
+  auto issue_a = [&](uint8_t* ta, uint32_t k) __attribute__((always_inline)) {
+    if (KTail && kAK && k == ksteps - 1)
+      issue_tile_k_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
+    else
+      issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
+  };
+  auto issue_b = [&](uint8_t* tb, uint32_t k) __attribute__((always_inline)) {
+    if (KTail && kBK_ && k == ksteps - 1)
+      issue_tile_k_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
+    else
+      issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
+  };
   auto fetch = [&](uint8_t* ta, uint8_t* tb, uint32_t k) {
-    issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
-    issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
+    issue_a(ta, k);
+    issue_b(tb, k);
   };
   // Prologue: K steps 0 and 1 (clamped: K = 64 re-fetches step 0 into a
   // stage that is never read).
@@ -281,12 +329,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     // has landed; after the barrier, every wave's have.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue_tile<BK>(a_rsrc, ta, wave, a_voff, clamp(kt + 2) * a_kstep);
+    issue_a(ta, clamp(kt + 2));
     read_sub(na, nb, 0, 0);
     mma(2);
     sched(kDma);
     __builtin_amdgcn_sched_barrier(0);
-    issue_tile<BK>(b_rsrc, tb, wave, b_voff, clamp(kt + 2) * b_kstep);
+    issue_b(tb, clamp(kt + 2));
     read_sub(na, nb, 1, 1);
     mma(3);
     sched(kDma);
@@ -328,7 +376,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   for (int k = 0; k < 32; ++k) {
     const uint32_t v = k * kWave + lane, r = v / 16, c = v % 16;
     const u32x4 x = *reinterpret_cast<const u32x4*>(cst + r * 256 + ((c ^ (r & 15)) << 4));
-    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(cw + (uint64_t)r * N + c * 8));
+    // Rows past M and 8-column chunks past N (N % 8 == 0) are not stored.
+    if (m0 + wm + r < M && n0 + wn + c * 8 < N)
+      __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(cw + (uint64_t)r * N + c * 8));
   }
 }
 
@@ -380,10 +430,17 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
 
 template <bool TL, bool TR, bool G>
 int launch_fast(hipStream_t stream, const GemmArgs& a) {
-  const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
-  hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G>), dim3(tiles, a.batches), dim3(kThreads), 0,
-                     stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
-                     a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
+  if (a.inner % 64 == 0)
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, false>), dim3(tiles, a.batches),
+                       dim3(kThreads), 0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
+                       (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
+                       a.right_batch_stride);
+  else
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, true>), dim3(tiles, a.batches),
+                       dim3(kThreads), 0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
+                       (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
+                       a.right_batch_stride);
   return hip_status(hipGetLastError());
 }
 
@@ -407,10 +464,11 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   const uint64_t a_span = a.transpose_left ? (uint64_t)a.inner * a.rows * 2 : 256ull * a.inner * 2;
   const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
   const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
-  if (aligned && fits && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner > 0) {
-    if (a.inner % 64 == 0)
-      return a.gelu ? dispatch_fast<true>(stream, a) : dispatch_fast<false>(stream, a);
-  }
+  // Any M and N: rows past the edge read as 0 and are not stored.  16-byte
+  // chunks need N and K (and M when A is transposed) to be multiples of 8.
+  const bool chunked = a.inner % 8 == 0 && a.columns % 8 == 0 && (!a.transpose_left || a.rows % 8 == 0);
+  if (aligned && fits && chunked && a.inner > 0)
+    return a.gelu ? dispatch_fast<true>(stream, a) : dispatch_fast<false>(stream, a);
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
                      stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,

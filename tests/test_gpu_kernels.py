@@ -220,6 +220,23 @@ def test_gemm_f16_transposes(ipus, oracle, ctx, tl, tr, M, N, K):
     assert fp16_close(got, want, FP16_TOL)
 
 
+@pytest.mark.parametrize("tl", [False, True])
+@pytest.mark.parametrize("tr", [False, True])
+@pytest.mark.parametrize("M,N,K", [(729, 4304, 1152), (729, 1152, 4304), (264, 520, 72),
+                                   (257, 264, 136), (8, 8, 8)])
+def test_gemm_f16_ragged_tiles(ipus, oracle, ctx, tl, tr, M, N, K):
+    """Shapes off the 256 x 256 x 64 grid (the reference's SigLIP MLP: 729 tokens,
+    width 1152, hidden 4304): partial tiles along M and N and a partial last K
+    step, in all four operand layouts."""
+    got, want = gemm_case(ipus, oracle, ctx, M, N, K, tl, tr)
+    assert fp16_close(got, want, FP16_TOL)
+
+
+def test_gemm_f16_ragged_batched(ipus, oracle, ctx):
+    got, want = gemm_case(ipus, oracle, ctx, 300, 136, 200, batches=3)
+    assert fp16_close(got, want, FP16_TOL)
+
+
 @pytest.mark.parametrize("bl,br", [(True, True), (True, False), (False, True)])
 def test_gemm_f16_batched_broadcast(ipus, oracle, ctx, bl, br):
     got, want = gemm_case(ipus, oracle, ctx, 256, 256, 128, batches=3, bl=bl, br=br)
