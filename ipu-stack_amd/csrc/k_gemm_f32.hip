@@ -2,7 +2,10 @@
 // output: replaces gemm_f32_64_amp (device/gemm_f32_64_amp.S:125-385), whose
 // init mode clears the output and accumulates in fp32 (gemm_f32_64_amp.S:40-56).
 //
-// Fast kernel (M % 128 == 0, N % 128 == 0, K % 32 == 0):
+// Fast kernel (16-byte aligned operands whose contiguous axes, and N, are
+// multiples of 4; the Edge
+// instantiation, used off the 128 x 128 x 32 grid, zero-fills loads past M,
+// N or K and stores only rows < M and 4-column chunks < N):
 //   * block tile 128 x 128 x 32, 4 waves in a 2 x 2 grid, each wave 64 x 64
 //     as 2 x 2 MFMA tiles;
 //   * operands staged in LDS k-major ([k][m], [k][n]) so a fragment is 32
@@ -34,18 +37,26 @@ __device__ __forceinline__ uint32_t swz32(uint32_t k, uint32_t x) {
 // Loads a 128 (x) by 32 (k) operand tile.
 // XContig: element (x, k) at base[(k0 + k) * ld + x0 + x]  (stored [K][X])
 // else:    element (x, k) at base[(x0 + x) * ld + k0 + k]  (stored [X][K])
-template <bool XContig>
+// Edge: chunks of 4 floats past X (x extent) or K read as 0 (X and K are
+// multiples of 4, so a chunk is wholly inside or outside).
+template <bool XContig, bool Edge>
 __device__ __forceinline__ void load_tile32(const float* __restrict__ base, uint64_t ld,
-                                            uint32_t x0, uint32_t k0, u32x4 v[4]) {
+                                            uint32_t x0, uint32_t k0, u32x4 v[4], uint32_t X,
+                                            uint32_t K) {
   const uint32_t t = threadIdx.x;
+  const u32x4 zero = {0, 0, 0, 0};
   if constexpr (XContig) {
-    const float* p = base + (uint64_t)(k0 + t / 32) * ld + x0 + (t % 32) * 4;
+    const uint32_t k = k0 + t / 32, x = x0 + (t % 32) * 4;
+    const float* p = base + (uint64_t)k * ld + x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = load16(p + (uint64_t)(8 * i) * ld);
+    for (int i = 0; i < 4; ++i)
+      v[i] = !Edge || (k + 8 * i < K && x < X) ? load16(p + (uint64_t)(8 * i) * ld) : zero;
   } else {
-    const float* p = base + (uint64_t)(x0 + (t / 8) * 4) * ld + k0 + (t % 8) * 4;
+    const uint32_t x = x0 + (t / 8) * 4, k = k0 + (t % 8) * 4;
+    const float* p = base + (uint64_t)x * ld + k;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = load16(p + (uint64_t)j * ld);
+    for (int j = 0; j < 4; ++j)
+      v[j] = !Edge || (x + j < X && k < K) ? load16(p + (uint64_t)j * ld) : zero;
   }
 }
 
@@ -70,13 +81,13 @@ __device__ __forceinline__ float read32(const uint8_t* lds, uint32_t k, uint32_t
   return *reinterpret_cast<const float*>(lds + swz32(k, x));
 }
 
-template <bool TransposeLeft, bool TransposeRight>
+template <bool TransposeLeft, bool TransposeRight, bool Edge>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_128_kernel(
     float* __restrict__ out, const float* __restrict__ left, const float* __restrict__ right,
     uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kTileBytes];
 
-  const uint32_t nbm = M / kBM, nbn = N / kBN;
+  const uint32_t nbm = (M + kBM - 1) / kBM, nbn = (N + kBN - 1) / kBN;
   const uint32_t tiles = nbm * nbn;
   uint32_t pid = blockIdx.x;
   if (tiles % 8 == 0) pid = (pid % 8) * (tiles / 8) + pid / 8;
@@ -110,19 +121,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_128_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   u32x4 ra[4], rb[4];
-  load_tile32<kAX>(A, lda, m0, 0, ra);
-  load_tile32<kBX>(B, ldb, n0, 0, rb);
+  load_tile32<kAX, Edge>(A, lda, m0, 0, ra, M, K);
+  load_tile32<kBX, Edge>(B, ldb, n0, 0, rb, N, K);
   store_tile32<kAX>((smem + 0 + (0) * 2 * kTileBytes), ra);
   store_tile32<kBX>((smem + kTileBytes + (0) * 2 * kTileBytes), rb);
   __syncthreads();
 
-  const uint32_t ksteps = K / kBK;
+  const uint32_t ksteps = (K + kBK - 1) / kBK;
   for (uint32_t kt = 0; kt < ksteps; ++kt) {
     const uint32_t cur = kt & 1;
     const bool more = kt + 1 < ksteps;
     if (more) {
-      load_tile32<kAX>(A, lda, m0, (kt + 1) * kBK, ra);
-      load_tile32<kBX>(B, ldb, n0, (kt + 1) * kBK, rb);
+      load_tile32<kAX, Edge>(A, lda, m0, (kt + 1) * kBK, ra, M, K);
+      load_tile32<kBX, Edge>(B, ldb, n0, (kt + 1) * kBK, rb, N, K);
     }
     const uint8_t* la = (smem + 0 + (cur) * 2 * kTileBytes);
     const uint8_t* lb = (smem + kTileBytes + (cur) * 2 * kTileBytes);
@@ -148,13 +159,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_128_kernel(
   }
 
   const uint32_t row = m0 + wm + lane % 32;
+  const uint32_t col = n0 + wn + 4 * (lane / 32);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    float* crow = C + (uint64_t)(row + 32 * i) * N + n0 + wn + 4 * (lane / 32);
+    if (Edge && row + 32 * i >= M) continue;
+    float* crow = C + (uint64_t)(row + 32 * i) * N + col;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (Edge && col + 32 * j + 8 * g >= N) continue;
         float4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
@@ -211,10 +225,16 @@ __global__ __launch_bounds__(256) void gemm_f32_general_kernel(
 
 template <bool TL, bool TR>
 int launch_fast(hipStream_t stream, const GemmArgs& a) {
-  const uint32_t tiles = (a.rows / kBM) * (a.columns / kBN);
-  hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR>), dim3(tiles, a.batches), dim3(kThreads), 0,
-                     stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
-                     a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
+  const bool grid = a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner % kBK == 0;
+  if (grid)
+    hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR, false>), dim3(tiles, a.batches), dim3(kThreads),
+                       0, stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
+                       a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  else
+    hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR, true>), dim3(tiles, a.batches), dim3(kThreads),
+                       0, stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
+                       a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
   return hip_status(hipGetLastError());
 }
 
@@ -226,7 +246,11 @@ int launch_gemm_f32(hipStream_t stream, const GemmArgs& a) {
   const bool aligned = ((uintptr_t)a.left % 16 == 0) && ((uintptr_t)a.right % 16 == 0) &&
                        ((uintptr_t)a.out % 16 == 0) && a.left_batch_stride % 4 == 0 &&
                        a.right_batch_stride % 4 == 0;
-  if (aligned && a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner % kBK == 0 && a.inner > 0) {
+  // 4-float chunks run along the contiguous axis of each operand and of C:
+  // N always, K for row-major A or transposed B, M for transposed A.
+  const bool chunked = a.columns % 4 == 0 && (a.transpose_left ? a.rows % 4 == 0 : a.inner % 4 == 0) &&
+                       (!a.transpose_right || a.inner % 4 == 0);
+  if (aligned && chunked && a.inner > 0) {
     if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
     if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
     if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);

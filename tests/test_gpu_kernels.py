@@ -288,7 +288,12 @@ def test_gemm_f16_8192_sampled_rows(ipus, oracle, ctx):
 @pytest.mark.parametrize("M,N,K,tl,tr", [(128, 128, 32, False, False), (256, 384, 96, False, False),
                                          (128, 256, 64, True, False), (128, 256, 64, False, True),
                                          (128, 256, 64, True, True), (33, 17, 9, False, False),
-                                         (65, 130, 70, True, True)])
+                                         (65, 130, 70, True, True),
+                                         # partial tiles on the fast kernel
+                                         (132, 260, 36, False, False), (132, 260, 36, True, False),
+                                         (132, 260, 36, False, True), (300, 4, 1100, True, True),
+                                         (4, 516, 20, False, False), (729, 1152, 36, False, False),
+                                         (729, 132, 36, False, True)])
 def test_gemm_f32(ipus, oracle, ctx, M, N, K, tl, tr):
     a = ipus.synth_f32(M * K, 31, 1, 1)
     b = ipus.synth_f32(K * N, 31, 2, 1)
