@@ -112,6 +112,20 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        ipu_stack_gemm_f16 followed by ipu_stack_gelu_tanh_approx_f16).  No
  *        reference symbol: build_package fuses a Gemm whose result feeds only
  *        one Gelu (graph.rs:315-331) into this launch.
+ *   ipu_stack_gemm_f16_split           out fp32 partials
+ *        float[splits][batches][rows][columns]; inputs as ipu_stack_gemm_f16;
+ *        scalars as ipu_stack_gemm_f16 plus splits: split z sums k in
+ *        [z c, (z + 1) c), c = 64 * ceil(ceil(inner / splits) / 64), and
+ *        ceil(inner / c) must equal splits.  Needs the 256 x 256 kernel's
+ *        conditions (16-byte aligned operands; columns and inner, and rows
+ *        when the left operand is transposed, multiples of 8), else
+ *        IPUS_ERROR_UNAVAILABLE.  No reference symbol (the reference's
+ *        split-K is the ParallelReduction plan, operator.rs:307-347):
+ *        build_package plans it for few-tile, long-K GEMMs.
+ *   ipu_stack_reduce_splits_f16        out f16; input the fp32 partials;
+ *        splits, element_count (a multiple of 8), gelu (0/1): the sum over
+ *        splits in order, rounded to fp16 once (GELU of that value when
+ *        gelu = 1, as in ipu_stack_gemm_f16_gelu).
  *   ipu_stack_gemm_f32                 as above in fp32
  *        (device/gemm_f32_64_amp.S:125-385).
  *   ipu_stack_flash_attention_online_f16  out (f32 or f16); query, key,

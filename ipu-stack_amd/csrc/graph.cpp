@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "kernels.h"
 
 using namespace ipus;
 
@@ -584,6 +585,25 @@ int build_error(const std::string& message) {
   return fail(IPUS_ERROR_BUILD, "%s", message.c_str());
 }
 
+// Split-K count for an fp16 GEMM on the 256 x 256 kernel: min(16, K / 1024,
+// 64 / tiles), i.e. only for outputs of at most 32 tiles and K >= 2048, with
+// every split keeping >= 1024 k and about 64 workgroups in all (measured:
+// 729 x 1152 x 4304 115 -> 45 us at 4 splits, 256 x 256 x 8192 132 -> 32 us
+// at 8, 1024 x 1024 x 8192 134 -> 59 us at 4; more splits lose to the fp32
+// partials' traffic).  Returns 1 (no split) when the shape is outside the
+// fast kernel's reach.
+uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K, uint64_t batches, bool tl, bool tr) {
+  if (K < 2048 || K % 8 != 0 || N % 8 != 0 || (tl && M % 8 != 0)) return 1;
+  const uint64_t a_span = tl ? (uint64_t)K * M * 2 : 256ull * K * 2;
+  const uint64_t b_span = tr ? 256ull * K * 2 : (uint64_t)K * N * 2;
+  if (a_span >= (1ull << 31) || b_span >= (1ull << 31)) return 1;
+  const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256) * batches;
+  const uint64_t want = std::min<uint64_t>({16, K / 1024, 64 / tiles});
+  if (want < 2) return 1;
+  const uint32_t chunk = (uint32_t)gemm_f16_split_chunk(K, (uint32_t)want);
+  return (K + chunk - 1) / chunk;  // every split owns some k
+}
+
 struct Builder {
   const ipus_graph& g;
   ipus_package_config cfg;
@@ -670,6 +690,22 @@ struct Builder {
         // matrix; otherwise one launch per output batch.
         if ((lcount == batches || lcount == 1) && (rcount == batches || rcount == 1) &&
             batches <= 65535) {
+          if (cp == IPUS_PRECISION_F16) {
+            const uint32_t splits = gemm_splits(M, N, K, batches, op.transpose_left,
+                                                op.transpose_right);
+            if (splits > 1) {
+              // Few output tiles, long K: split K over more workgroups into
+              // fp32 partials (an arena value), then sum and round once.
+              const int parts = new_slot({splits * (uint32_t)batches, M, N}, IPUS_PRECISION_F32);
+              emit("ipu_stack_gemm_f16_split", parts, {{l, 0}, {r, 0}},
+                   {(uint32_t)batches, M, N, K, op.transpose_left ? 1u : 0u,
+                    op.transpose_right ? 1u : 0u, (uint32_t)(lcount == 1 ? 0 : lm),
+                    (uint32_t)(rcount == 1 ? 0 : rm), splits});
+              emit("ipu_stack_reduce_splits_f16", out, {{parts, 0}},
+                   {splits, (uint32_t)(batches * M * N), 0u});
+              return 0;
+            }
+          }
           emit(sym, out, {{l, 0}, {r, 0}},
                {(uint32_t)batches, M, N, K, op.transpose_left ? 1u : 0u,
                 op.transpose_right ? 1u : 0u, (uint32_t)(lcount == 1 ? 0 : lm),
@@ -868,7 +904,11 @@ void fuse_gemm_gelu(ipus_package& pkg) {
   std::vector<Step> steps;
   for (size_t i = 0; i < pkg.steps.size(); ++i) {
     const Step& s = pkg.steps[i];
-    if (i + 1 < pkg.steps.size() && s.symbol == "ipu_stack_gemm_f16" && s.out.byte_offset == 0) {
+    // The split-K reduction (the last step of a split GEMM) fuses the same
+    // way: it rounds each sum to fp16 before GELU.
+    const bool split_reduce = s.symbol == "ipu_stack_reduce_splits_f16" && s.scalars[2] == 0;
+    if (i + 1 < pkg.steps.size() && (s.symbol == "ipu_stack_gemm_f16" || split_reduce) &&
+        s.out.byte_offset == 0) {
       const Step& n = pkg.steps[i + 1];
       const int mid = s.out.slot;
       const Slot& ms = pkg.slots[(size_t)mid];
@@ -877,7 +917,10 @@ void fuse_gemm_gelu(ipus_package& pkg) {
           !ms.external && writes[(size_t)mid] == 1 && reads[(size_t)mid] == 1 &&
           n.scalars[0] == elements(ms.storage.shape)) {
         Step f = s;
-        f.symbol = "ipu_stack_gemm_f16_gelu";
+        if (split_reduce)
+          f.scalars[2] = 1;
+        else
+          f.symbol = "ipu_stack_gemm_f16_gelu";
         f.out = n.out;
         steps.push_back(std::move(f));
         ++i;

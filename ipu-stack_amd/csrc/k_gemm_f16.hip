@@ -159,11 +159,15 @@ __device__ __forceinline__ half_t epilogue(float acc) {
   return h;
 }
 
-template <bool TransposeLeft, bool TransposeRight, bool Gelu, bool KTail>
+// Split: workgroup z covers K range [z k_chunk, (z + 1) k_chunk) (k_chunk a
+// multiple of 64) and writes its fp32 partial tile to out viewed as
+// float[splits][batches][M][N] (ipu_stack_gemm_f16_split); otherwise
+// k_chunk == K and out is the fp16 C.
+template <bool TransposeLeft, bool TransposeRight, bool Gelu, bool KTail, bool Split>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
     const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
-    uint64_t left_batch_stride, uint64_t right_batch_stride) {
+    uint64_t left_batch_stride, uint64_t right_batch_stride, uint32_t k_chunk) {
   constexpr int BK = 64;
   constexpr int kTileBytes = Tile<BK>::kBytes;
   constexpr int kDma = Tile<BK>::kDmaPerWave;
@@ -194,9 +198,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   const uint16_t* B = right + batch * right_batch_stride;
   uint16_t* C = out + batch * (uint64_t)M * N;
 
-  // Buffer descriptors based at this block's first row / column.
-  const uint16_t* a_base = kAK ? A + (uint64_t)m0 * K : A + m0;
-  const uint16_t* b_base = kBK_ ? B + (uint64_t)n0 * K : B + n0;
+  // This workgroup's K range (the whole of K unless Split).
+  const uint32_t k_begin = Split ? blockIdx.z * k_chunk : 0;
+  const uint32_t k_len = Split ? (K - k_begin < k_chunk ? K - k_begin : k_chunk) : K;
+
+  // Buffer descriptors based at this block's first row / column and first
+  // k; their ranges run to the operand's end.
+  const uint16_t* a_base = kAK ? A + (uint64_t)m0 * K + k_begin : A + m0 + (uint64_t)k_begin * M;
+  const uint16_t* b_base = kBK_ ? B + (uint64_t)n0 * K + k_begin : B + n0 + (uint64_t)k_begin * N;
   const uint64_t a_bytes = (uint64_t)M * K * 2 - (uint64_t)(a_base - A) * 2;
   const uint64_t b_bytes = (uint64_t)N * K * 2 - (uint64_t)(b_base - B) * 2;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -225,21 +234,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const uint32_t ksteps = (K + BK - 1) / BK;
+  const uint32_t ksteps = (k_len + BK - 1) / BK;
   // K-contiguous operands mask the chunks past K on the last step (MN-
   // contiguous rows past K are past the buffer's range).
-  const uint32_t k_tail = K % BK;
+  const uint32_t k_tail = k_len % BK;  // nonzero only on the last split
   auto clamp = [&](uint32_t k) { return k < ksteps ? k : ksteps - 1; };
   // KTail (K % BK != 0) is a separate instantiation, so the branch never
   // enters the scheduled K loop of the common case.
   auto issue_a = [&](uint8_t* ta, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && kAK && k == ksteps - 1)
+    if (KTail && kAK && k_tail != 0 && k == ksteps - 1)
       issue_tile_k_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
     else
       issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
   };
   auto issue_b = [&](uint8_t* tb, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && kBK_ && k == ksteps - 1)
+    if (KTail && kBK_ && k_tail != 0 && k == ksteps - 1)
       issue_tile_k_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
     else
       issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
@@ -348,6 +357,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   if (kt < ksteps) step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the redundant prefetches
 
+  if constexpr (Split) {
+    // fp32 partial tile, 16-byte stores of 4 consecutive columns.
+    float* P = reinterpret_cast<float*>(out) +
+               ((uint64_t)blockIdx.z * gridDim.y + batch) * (uint64_t)M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = m0 + wm + 32 * i + lane % 32;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t col = n0 + wn + 32 * j + 8 * g + 4 * (lane / 32);
+          if (col >= N) continue;
+          float4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+          __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(P + (uint64_t)row * N + col));
+        }
+    }
+    return;
+  }
+
   // The wave's 128 x 128 fp16 result goes through its own quarter of the
   // (now idle) LDS stages, so that it reaches memory as 256-byte row runs
   // written by 16 lanes with streaming stores instead of 16-byte pieces of
@@ -428,47 +460,112 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
   }
 }
 
-template <bool TL, bool TR, bool G>
-int launch_fast(hipStream_t stream, const GemmArgs& a) {
+template <bool TL, bool TR, bool G, bool Split>
+int launch_fast(hipStream_t stream, const GemmArgs& a, uint32_t splits, uint32_t k_chunk) {
   const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
+  const dim3 grid(tiles, a.batches, splits);
   if (a.inner % 64 == 0)
-    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, false>), dim3(tiles, a.batches),
-                       dim3(kThreads), 0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
-                       (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
-                       a.right_batch_stride);
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, false, Split>), grid, dim3(kThreads), 0,
+                       stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
+                       a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride,
+                       k_chunk);
   else
-    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, true>), dim3(tiles, a.batches),
-                       dim3(kThreads), 0, stream, (uint16_t*)a.out, (const uint16_t*)a.left,
-                       (const uint16_t*)a.right, a.rows, a.columns, a.inner, a.left_batch_stride,
-                       a.right_batch_stride);
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, true, Split>), grid, dim3(kThreads), 0,
+                       stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
+                       a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride,
+                       k_chunk);
   return hip_status(hipGetLastError());
 }
 
-template <bool G>
-int dispatch_fast(hipStream_t stream, const GemmArgs& a) {
-  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false, G>(stream, a);
-  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true, G>(stream, a);
-  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false, G>(stream, a);
-  return launch_fast<true, true, G>(stream, a);
+template <bool G, bool Split>
+int dispatch_fast(hipStream_t stream, const GemmArgs& a, uint32_t splits, uint32_t k_chunk) {
+  if (!a.transpose_left && !a.transpose_right)
+    return launch_fast<false, false, G, Split>(stream, a, splits, k_chunk);
+  if (!a.transpose_left && a.transpose_right)
+    return launch_fast<false, true, G, Split>(stream, a, splits, k_chunk);
+  if (a.transpose_left && !a.transpose_right)
+    return launch_fast<true, false, G, Split>(stream, a, splits, k_chunk);
+  return launch_fast<true, true, G, Split>(stream, a, splits, k_chunk);
+}
+
+// Conditions of the 256 x 256 kernel: 16-byte aligned operands, 32-bit
+// per-block buffer offsets, 16-byte chunks (N and K, and M when A is
+// transposed, multiples of 8).
+bool fast_ok(const GemmArgs& a) {
+  const bool aligned = ((uintptr_t)a.left % 16 == 0) && ((uintptr_t)a.right % 16 == 0) &&
+                       ((uintptr_t)a.out % 16 == 0) && a.left_batch_stride % 8 == 0 &&
+                       a.right_batch_stride % 8 == 0;
+  const uint64_t a_span = a.transpose_left ? (uint64_t)a.inner * a.rows * 2 : 256ull * a.inner * 2;
+  const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
+  const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
+  const bool chunked = a.inner % 8 == 0 && a.columns % 8 == 0 && (!a.transpose_left || a.rows % 8 == 0);
+  return aligned && fits && chunked && a.inner > 0;
+}
+
+// fp32 partials [splits][count] -> fp16 (optionally GELU of the fp16 value):
+// 8 elements per thread, splits summed in order.
+__global__ __launch_bounds__(256) void reduce_splits_f16_kernel(uint16_t* __restrict__ out,
+                                                                const float* __restrict__ parts,
+                                                                uint32_t splits, uint64_t count,
+                                                                bool gelu) {
+  const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= count) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (uint32_t s = 0; s < splits; ++s) {
+    const float* p = parts + (uint64_t)s * count + i;
+    const float4_t lo = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(p));
+    const float4_t hi = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(p + 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] += lo[e];
+      acc[4 + e] += hi[e];
+    }
+  }
+  half8_t h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = gelu ? epilogue<true>(acc[e]) : epilogue<false>(acc[e]);
+  *reinterpret_cast<half8_t*>(out + i) = h;
 }
 
 }  // namespace
 
+int gemm_f16_split_chunk(uint32_t inner, uint32_t splits) {
+  if (splits == 0 || inner == 0) return 0;
+  const uint32_t per = (inner + splits - 1) / splits;
+  return (int)((per + 63) / 64 * 64);
+}
+
+int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits) {
+  if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
+  if (a.batches > 65535 || splits == 0 || splits > 64 || a.gelu) return IPUS_ERROR_INVALID_ARGUMENT;
+  if (!fast_ok(a)) return IPUS_ERROR_UNAVAILABLE;
+  const uint32_t k_chunk = (uint32_t)gemm_f16_split_chunk(a.inner, splits);
+  // Every split must own at least one k: the plan picks splits so that
+  // ceil(K / k_chunk) == splits.
+  if ((a.inner + k_chunk - 1) / k_chunk != splits) return IPUS_ERROR_INVALID_ARGUMENT;
+  return dispatch_fast<false, true>(stream, a, splits, k_chunk);
+}
+
+int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
+                             uint64_t count, bool gelu) {
+  if (count == 0) return 0;
+  if (splits == 0 || count % 8 != 0 || (uintptr_t)dst % 16 != 0 || (uintptr_t)parts % 16 != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  const uint64_t blocks = (count / 8 + 255) / 256;
+  if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(reduce_splits_f16_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                     (uint16_t*)dst, (const float*)parts, splits, count, gelu);
+  return hip_status(hipGetLastError());
+}
+
 int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
   if (a.batches > 65535) return IPUS_ERROR_INVALID_ARGUMENT;
-  const bool aligned = ((uintptr_t)a.left % 16 == 0) && ((uintptr_t)a.right % 16 == 0) &&
-                       ((uintptr_t)a.out % 16 == 0) && a.left_batch_stride % 8 == 0 &&
-                       a.right_batch_stride % 8 == 0;
-  // Buffer offsets are 32-bit: per-block offsets stay below 2^31 bytes.
-  const uint64_t a_span = a.transpose_left ? (uint64_t)a.inner * a.rows * 2 : 256ull * a.inner * 2;
-  const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
-  const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
-  // Any M and N: rows past the edge read as 0 and are not stored.  16-byte
-  // chunks need N and K (and M when A is transposed) to be multiples of 8.
-  const bool chunked = a.inner % 8 == 0 && a.columns % 8 == 0 && (!a.transpose_left || a.rows % 8 == 0);
-  if (aligned && fits && chunked && a.inner > 0)
-    return a.gelu ? dispatch_fast<true>(stream, a) : dispatch_fast<false>(stream, a);
+  // Any M and N on the fast kernel: rows past the edge read as 0 and are not
+  // stored.
+  if (fast_ok(a))
+    return a.gelu ? dispatch_fast<true, false>(stream, a, 1, a.inner)
+                  : dispatch_fast<false, false>(stream, a, 1, a.inner);
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
                      stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,

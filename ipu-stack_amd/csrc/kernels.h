@@ -37,6 +37,14 @@ struct AttentionArgs {
 
 // Dense products (k_gemm_f16.hip, k_gemm_f32.hip).
 int launch_gemm_f16(hipStream_t stream, const GemmArgs& a);
+// Split-K: fp32 partials float[splits][batches][M][N] into a.out (a.gelu must
+// be false), then launch_reduce_splits_f16 to fp16.  gemm_f16_split_chunk
+// gives the k range per split (a multiple of 64); the plan picks splits so
+// that every split owns some k.
+int gemm_f16_split_chunk(uint32_t inner, uint32_t splits);
+int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits);
+int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
+                             uint64_t count, bool gelu);
 int launch_gemm_f32(hipStream_t stream, const GemmArgs& a);
 
 // Fused online-softmax attention (k_attention.hip).

@@ -333,6 +333,33 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return run_gemm(c, o, i, s, true, true);
        }},
+      // Split-K GEMM (no reference counterpart; planned by build_package for
+      // few-tile, long-K shapes): fp32 partials float[splits][batches][M][N].
+      {"ipu_stack_gemm_f16_split", 2,
+       {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
+        "left_batch_stride", "right_batch_stride", "splits"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         if (s[4] > 1 || s[5] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+         GemmArgs a;
+         a.out = o;
+         a.left = i[0];
+         a.right = i[1];
+         a.batches = s[0];
+         a.rows = s[1];
+         a.columns = s[2];
+         a.inner = s[3];
+         a.transpose_left = s[4] != 0;
+         a.transpose_right = s[5] != 0;
+         a.left_batch_stride = s[6];
+         a.right_batch_stride = s[7];
+         return launch_gemm_f16_split(c->stream, a, s[8]);
+       }},
+      // Sum of the split partials rounded to fp16 (GELU of it when gelu = 1).
+      {"ipu_stack_reduce_splits_f16", 1, {"splits", "element_count", "gelu"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         if (s[2] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+         return launch_reduce_splits_f16(c->stream, o, i[0], s[0], s[1], s[2] != 0);
+       }},
       {"ipu_stack_gemm_f32", 2,
        {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
         "left_batch_stride", "right_batch_stride"},

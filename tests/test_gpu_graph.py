@@ -63,6 +63,63 @@ def test_mlp_package_matches_oracle_and_fusion_is_exact(ipus, oracle, ctx):
         b.free()
 
 
+def test_split_k_mlp_package_matches_oracle(ipus, oracle, ctx):
+    """The reference's SigLIP MLP at one image (729 tokens, width 1152, hidden
+    4304): the second GEMM is planned split-K with GELU fused into the
+    reduction."""
+    m, d, h = 729, 1152, 4304
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [m, d])
+    w1 = g.parameter("w1", [d, h])
+    w2 = g.parameter("w2", [h, d])
+    g.set_outputs([g.gelu(g.gemm(g.gelu(g.gemm(x, w1)), w2))])
+    xs = synth(ipus, m * d, 33, 1).reshape(m, d)
+    w1s = synth(ipus, d * h, 33, 2, scale=0.05).reshape(d, h)
+    w2s = synth(ipus, h * d, 33, 3, scale=0.05).reshape(h, d)
+    pkg, (y,) = run_package(ipus, ctx, g, {"x": xs, "w1": w1s, "w2": w2s})
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16_split",
+                                         "ipu_stack_reduce_splits_f16"]
+    hidden = oracle.gelu_f16(oracle.gemm_f16(xs, w1s, m, h, d)).reshape(m, h)
+    want = oracle.f16_to_f32(oracle.gelu_f16(oracle.gemm_f16(hidden, w2s, m, d, h))).reshape(m, d)
+    assert fp16_close(oracle.f16_to_f32(y), want, FP16_TOL)
+
+
+@pytest.mark.parametrize("M,N,K,tl,tr,splits,batches", [
+    (729, 1152, 4304, 0, 0, 8, 1), (729, 1152, 4304, 0, 1, 8, 1), (264, 136, 3000, 0, 1, 5, 2),
+    (200, 264, 2048, 1, 0, 4, 1), (256, 256, 4096, 0, 0, 16, 1)])
+def test_split_k_gemm_matches_oracle(ipus, oracle, ctx, M, N, K, tl, tr, splits, batches):
+    """Split partials summed by the reduction equal the one-launch GEMM's
+    semantics (fp32 accumulation, one fp16 rounding) to the fp16 bar, and the
+    GELU variant of the reduction is GELU of the plain reduction bit for bit."""
+    a = synth(ipus, batches * M * K, 34, 1)
+    b = synth(ipus, batches * K * N, 34, 2, scale=0.2)
+    ba, bb = ctx.upload(a), ctx.upload(b)
+    parts = ctx.alloc(splits * batches * M * N * 4)
+    out, act, fused = (ctx.alloc(batches * M * N * 2) for _ in range(3))
+    ctx.launch("ipu_stack_gemm_f16_split", parts, [ba, bb],
+               [batches, M, N, K, tl, tr, M * K, K * N, splits])
+    ctx.launch("ipu_stack_reduce_splits_f16", out, [parts], [splits, batches * M * N, 0])
+    ctx.launch("ipu_stack_reduce_splits_f16", fused, [parts], [splits, batches * M * N, 1])
+    ctx.launch("ipu_stack_gelu_tanh_approx_f16", act, [out], [batches * M * N])
+    got = oracle.f16_to_f32(out.download(np.uint16))
+    want = oracle.f16_to_f32(oracle.gemm_f16(a, b, M, N, K, bool(tl), bool(tr), batches,
+                                             M * K, K * N))
+    assert fp16_close(got, want, FP16_TOL)
+    assert np.array_equal(fused.download(np.uint16), act.download(np.uint16))
+    for buf in (ba, bb, parts, out, act, fused):
+        buf.free()
+
+
+def test_split_k_rejects_empty_splits(ipus, ctx):
+    buf = ctx.alloc(4096)
+    # K = 2048 in 3 splits of 704 k: ceil(2048 / 704) = 3, fine; 40 splits of
+    # 64 k leave 8 splits without work.
+    with pytest.raises(ipus.IpusError) as e:
+        ctx.launch("ipu_stack_gemm_f16_split", buf, [buf, buf], [1, 8, 8, 2048, 0, 0, 0, 0, 40])
+    assert e.value.status == ipus.ERROR_INVALID_ARGUMENT
+    buf.free()
+
+
 @pytest.mark.parametrize("M,N,K,tl,tr", [(256, 512, 128, 0, 0), (512, 256, 192, 1, 1),
                                          (100, 60, 40, 0, 0), (64, 96, 48, 0, 1)])
 def test_gemm_gelu_fusion_bit_exact(ipus, ctx, M, N, K, tl, tr):

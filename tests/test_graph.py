@@ -154,6 +154,38 @@ def test_build_package_mlp_plan(ipus):
     assert pkg.arena_bytes == 4096 * 16384 * 2
 
 
+def test_split_k_plan_for_few_tiles_and_long_k(ipus):
+    """The reference's SigLIP MLP at one image (729 tokens): its second GEMM has
+    3 x 5 output tiles and K = 4304, so it is split over K into fp32 partials
+    (an arena value) and summed; GELU after the first GEMM fuses into that
+    GEMM, a GELU after a split GEMM into the reduction."""
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [729, 1152])
+    w1 = g.parameter("w1", [1152, 4304])
+    w2 = g.parameter("w2", [4304, 1152])
+    g.set_outputs([g.gelu(g.gemm(g.gelu(g.gemm(x, w1)), w2))])
+    pkg = ipus.build_package(g)
+    syms = [s[0] for s in pkg.steps]
+    assert syms == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16_split",
+                    "ipu_stack_reduce_splits_f16"]
+    split, reduce = pkg.steps[1][2], pkg.steps[2][2]
+    assert split[:4] == (1, 729, 1152, 4304)
+    splits = split[8]
+    assert 2 <= splits <= 16
+    assert reduce == (splits, 729 * 1152, 1)  # GELU fused into the reduction
+    # Enough work per tile, or short K: no split.
+    g2 = ipus.ComputeGraph()
+    a = g2.host_input("a", [4096, 1024])
+    b = g2.parameter("b", [1024, 4096])
+    g2.set_outputs([g2.gemm(a, b)])
+    assert [s[0] for s in ipus.build_package(g2).steps] == ["ipu_stack_gemm_f16"]
+    g3 = ipus.ComputeGraph()
+    a = g3.host_input("a", [256, 512])
+    b = g3.parameter("b", [512, 256])
+    g3.set_outputs([g3.gemm(a, b)])
+    assert [s[0] for s in ipus.build_package(g3).steps] == ["ipu_stack_gemm_f16"]
+
+
 def test_gemm_gelu_fusion_needs_a_private_result(ipus):
     # The GEMM result is also an output: both launches stay.
     g = ipus.ComputeGraph()
