@@ -1276,6 +1276,7 @@ int launch_steps(ipus_session* s) {
 
 extern "C" int ipus_session_run(ipus_session* s) {
   if (!s) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null session");
+  if (int status = use_device(s->ctx)) return status;
   if (s->exec) {
     const hipError_t e = hipGraphLaunch(s->exec, s->ctx->stream);
     return e == hipSuccess ? 0 : hip_fail(e, "hipGraphLaunch");
@@ -1286,6 +1287,7 @@ extern "C" int ipus_session_run(ipus_session* s) {
 extern "C" int ipus_session_capture(ipus_session* s) {
   if (!s) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null session");
   if (s->exec || s->pkg->steps.empty()) return 0;
+  if (int status = use_device(s->ctx)) return status;
   hipStream_t stream = s->ctx->stream;
   hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");

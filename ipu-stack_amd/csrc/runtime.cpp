@@ -171,6 +171,7 @@ extern "C" int ipus_buffer_upload(ipus_context* ctx, void* dst, const void* src,
   if (!ctx || (!dst && bytes) || (!src && bytes))
     return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   if (!bytes) return 0;
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "upload");
@@ -181,6 +182,7 @@ extern "C" int ipus_buffer_download(ipus_context* ctx, void* dst, const void* sr
   if (!ctx || (!dst && bytes) || (!src && bytes))
     return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   if (!bytes) return 0;
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "download");
@@ -191,6 +193,7 @@ extern "C" int ipus_buffer_copy(ipus_context* ctx, void* dst, const void* src, s
   if (!ctx || (!dst && bytes) || (!src && bytes))
     return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   if (!bytes) return 0;
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "copy");
   return 0;
@@ -199,6 +202,7 @@ extern "C" int ipus_buffer_copy(ipus_context* ctx, void* dst, const void* src, s
 extern "C" int ipus_buffer_memset(ipus_context* ctx, void* ptr, int value, size_t bytes) {
   if (!ctx || (!ptr && bytes)) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   if (!bytes) return 0;
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipMemsetAsync(ptr, value, bytes, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "memset");
   return 0;
@@ -213,6 +217,7 @@ struct ipus_event {
 
 extern "C" int ipus_stream_sync(ipus_context* ctx) {
   if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   return 0;
@@ -240,6 +245,7 @@ extern "C" int ipus_event_destroy(ipus_event* ev) {
 
 extern "C" int ipus_event_record(ipus_context* ctx, ipus_event* ev) {
   if (!ctx || !ev) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (int status = use_device(ctx)) return status;
   hipError_t e = hipEventRecord(ev->event, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
   return 0;
