@@ -84,26 +84,31 @@ def test_split_k_mlp_package_matches_oracle(ipus, oracle, ctx):
     assert fp16_close(oracle.f16_to_f32(y), want, FP16_TOL)
 
 
-@pytest.mark.parametrize("M,N,K,tl,tr,splits,batches", [
-    (729, 1152, 4304, 0, 0, 8, 1), (729, 1152, 4304, 0, 1, 8, 1), (264, 136, 3000, 0, 1, 5, 2),
-    (200, 264, 2048, 1, 0, 4, 1), (256, 256, 4096, 0, 0, 16, 1)])
-def test_split_k_gemm_matches_oracle(ipus, oracle, ctx, M, N, K, tl, tr, splits, batches):
+@pytest.mark.parametrize("M,N,K,tl,tr,splits,batches,shared", [
+    (729, 1152, 4304, 0, 0, 8, 1, ""), (729, 1152, 4304, 0, 1, 8, 1, ""),
+    (264, 136, 3000, 0, 1, 5, 2, ""), (200, 264, 2048, 1, 0, 4, 1, ""),
+    (256, 256, 4096, 0, 0, 16, 1, ""), (264, 136, 3000, 0, 1, 5, 3, "right"),
+    (136, 264, 2560, 1, 1, 3, 2, "left")])
+def test_split_k_gemm_matches_oracle(ipus, oracle, ctx, M, N, K, tl, tr, splits, batches, shared):
     """Split partials summed by the reduction equal the one-launch GEMM's
     semantics (fp32 accumulation, one fp16 rounding) to the fp16 bar, and the
-    GELU variant of the reduction is GELU of the plain reduction bit for bit."""
-    a = synth(ipus, batches * M * K, 34, 1)
-    b = synth(ipus, batches * K * N, 34, 2, scale=0.2)
+    GELU variant of the reduction is GELU of the plain reduction bit for bit.
+    `shared` names an operand broadcast over the batch (batch stride 0)."""
+    lbs = 0 if shared == "left" else M * K
+    rbs = 0 if shared == "right" else K * N
+    a = synth(ipus, (1 if lbs == 0 else batches) * M * K, 34, 1)
+    b = synth(ipus, (1 if rbs == 0 else batches) * K * N, 34, 2, scale=0.2)
     ba, bb = ctx.upload(a), ctx.upload(b)
     parts = ctx.alloc(splits * batches * M * N * 4)
     out, act, fused = (ctx.alloc(batches * M * N * 2) for _ in range(3))
     ctx.launch("ipu_stack_gemm_f16_split", parts, [ba, bb],
-               [batches, M, N, K, tl, tr, M * K, K * N, splits])
+               [batches, M, N, K, tl, tr, lbs, rbs, splits])
     ctx.launch("ipu_stack_reduce_splits_f16", out, [parts], [splits, batches * M * N, 0])
     ctx.launch("ipu_stack_reduce_splits_f16", fused, [parts], [splits, batches * M * N, 1])
     ctx.launch("ipu_stack_gelu_tanh_approx_f16", act, [out], [batches * M * N])
     got = oracle.f16_to_f32(out.download(np.uint16))
     want = oracle.f16_to_f32(oracle.gemm_f16(a, b, M, N, K, bool(tl), bool(tr), batches,
-                                             M * K, K * N))
+                                             lbs, rbs))
     assert fp16_close(got, want, FP16_TOL)
     assert np.array_equal(fused.download(np.uint16), act.download(np.uint16))
     for buf in (ba, bb, parts, out, act, fused):

@@ -349,6 +349,18 @@ def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
     assert fp16_close(got, want, FP16_TOL)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("streams,sq,sk,d,dv", [(2, 50, 70, 160, 160), (1, 33, 45, 64, 96),
+                                                (2, 40, 40, 36, 36), (1, 20, 30, 256, 512),
+                                                (3, 65, 1, 128, 8)])
+def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d, dv):
+    """Widths the fast kernel does not take (query/key width above 128, value
+    width different from it, widths not a multiple of 8, value width up to
+    the general kernel's 512) run on the one-row-per-block kernel."""
+    got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal)
+    assert fp16_close(got, want, FP16_TOL)
+
+
 def test_attention_scale_and_f16_output(ipus, oracle, ctx):
     got, want = attention_case(ipus, oracle, ctx, 2, 256, 256, 128, 128, True, scale=0.05,
                                out_f16=True)
