@@ -186,6 +186,47 @@ def test_split_k_plan_for_few_tiles_and_long_k(ipus):
     assert [s[0] for s in ipus.build_package(g3).steps] == ["ipu_stack_gemm_f16"]
 
 
+def _single_gemm_package(ipus, m, n, k, config=None):
+    g = ipus.ComputeGraph()
+    a = g.host_input("a", [m, k])
+    b = g.parameter("b", [k, n])
+    g.set_outputs([g.gemm(a, b)])
+    return ipus.build_package(g, config) if config else ipus.build_package(g)
+
+
+@pytest.mark.parametrize("m,n,k,splits", [
+    # tiles = ceil(m/256) * ceil(n/256); splits = ceil(k / c) with
+    # c = 64 * ceil(ceil(k / want) / 64), want = min(16, k // 1024, 64 // tiles).
+    (729, 1152, 4304, 4),   # 15 tiles: want 4, c = 1088
+    (256, 256, 8192, 8),    # 1 tile: want 8, c = 1024
+    (1024, 1024, 8192, 4),  # 16 tiles: want 4, c = 2048
+    (64, 64, 40000, 16),    # 1 tile: want 16, c = 2560, 15.6 -> 16
+    (2048, 2048, 8192, 1),  # 64 tiles: want 1, one launch
+    (729, 1152, 1960, 1),   # k < 2048: one launch
+    (729, 1152, 4300, 1),   # k not a multiple of 8: one launch
+    (729, 1150, 4304, 1),   # n not a multiple of 8: one launch
+])
+def test_split_k_plan_counts(ipus, m, n, k, splits):
+    """The planner's split count for few-tile, long-K GEMMs, and the arena
+    room for the fp32 partials when it splits."""
+    pkg = _single_gemm_package(ipus, m, n, k)
+    syms = [s[0] for s in pkg.steps]
+    if splits == 1:
+        assert syms[0] != "ipu_stack_gemm_f16_split"
+        assert "ipu_stack_reduce_splits_f16" not in syms
+        return
+    assert syms == ["ipu_stack_gemm_f16_split", "ipu_stack_reduce_splits_f16"]
+    assert pkg.steps[0][2][8] == splits
+    assert pkg.steps[1][2] == (splits, m * n, 0)
+    assert pkg.arena_bytes >= splits * m * n * 4
+
+
+def test_split_k_not_planned_for_f32(ipus):
+    pkg = _single_gemm_package(ipus, 729, 1152, 4304, ipus.PackageConfig(compute_precision="f32"))
+    syms = [s[0] for s in pkg.steps]
+    assert "ipu_stack_gemm_f32" in syms and "ipu_stack_gemm_f16_split" not in syms
+
+
 def test_gemm_gelu_fusion_needs_a_private_result(ipus):
     # The GEMM result is also an output: both launches stay.
     g = ipus.ComputeGraph()
