@@ -299,6 +299,7 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_f16_scalar_kernel(
 // kernel); lane parity selects the row half, so each lane accumulates 8
 // rows; waves combine through LDS.  One launch, no workspace.
 constexpr uint32_t kReduceThreads = 256;
+constexpr int kReduceDepth = 4;  // loads in flight per thread (8 measured 5.4 TB/s)
 
 __global__ __launch_bounds__(kReduceThreads) void reduce_rows_block_major_kernel(
     float* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t columns,
@@ -328,14 +329,15 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_rows_block_major_kernel
     }
   };
   // v % 2 == threadIdx.x % 2 for every v a thread visits (the stride is
-  // even): each lane always sees the same row half.  Four loads in flight.
+  // even): each lane always sees the same row half.  kReduceDepth loads in
+  // flight; each lane adds its vectors in increasing v whatever the depth.
   uint32_t v = threadIdx.x;
-  for (; v + 3 * kReduceThreads < total_vectors; v += 4 * kReduceThreads) {
-    u32x4 x[4];
+  for (; v + (kReduceDepth - 1) * kReduceThreads < total_vectors; v += kReduceDepth * kReduceThreads) {
+    u32x4 x[kReduceDepth];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = load16_nt(src + element_of(v + u * kReduceThreads));
+    for (int u = 0; u < kReduceDepth; ++u) x[u] = load16_nt(src + element_of(v + u * kReduceThreads));
 #pragma unroll
-    for (int u = 0; u < 4; ++u) add8(x[u]);
+    for (int u = 0; u < kReduceDepth; ++u) add8(x[u]);
   }
   for (; v < total_vectors; v += kReduceThreads) add8(load16_nt(src + element_of(v)));
   // Reduce over lanes of equal parity.
