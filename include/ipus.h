@@ -86,6 +86,17 @@ int ipus_buffer_upload(ipus_context *context, void *device_dst, const void *host
                        size_t bytes);
 int ipus_buffer_download(ipus_context *context, void *host_dst, const void *device_src,
                          size_t bytes);
+/* Buffers allocated through the context and not yet freed (count, bytes).
+ * ipus_context_destroy releases any that remain.  No reference counterpart:
+ * it lets a caller check that an error path released what it allocated. */
+int ipus_context_live_buffers(ipus_context *context, uint64_t *count, uint64_t *bytes);
+/* Failure injection for tests of error propagation (the role of the
+ * reference's device timeouts and retry path, crates/ipu-tests/src/
+ * main.rs:985-1006, without a device fault): after `launches_before` more
+ * ipus_launch calls on this context, the next one returns `status` (< 0)
+ * without enqueuing work and the injection clears; status 0 cancels. */
+int ipus_context_inject_launch_failure(ipus_context *context, uint32_t launches_before,
+                                       int status);
 /* Stream-ordered device copy and byte fill. */
 int ipus_buffer_copy(ipus_context *context, void *device_dst, const void *device_src,
                      size_t bytes);

@@ -15,6 +15,7 @@ kernel-level ``Context.launch`` that mirrors one ComputeStep
 from __future__ import annotations
 
 import ctypes
+import weakref
 import os
 import struct
 from dataclasses import dataclass, field
@@ -124,6 +125,9 @@ _SIGNATURES = {
     "ipus_context_stream": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
     "ipus_buffer_alloc": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.POINTER(_P)]),
     "ipus_buffer_free": (ctypes.c_int, [_P, _P]),
+    "ipus_context_live_buffers": (
+        ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "ipus_context_inject_launch_failure": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_int]),
     "ipus_buffer_upload": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
     "ipus_buffer_download": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
     "ipus_buffer_copy": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
@@ -362,19 +366,27 @@ class Context:
         _check(_lib().ipus_context_create(int(device), ctypes.byref(h)))
         self.handle = h.value
         self._buffers: set[DeviceBuffer] = set()  # live buffers, freed by close()
+        self._sessions: "weakref.WeakSet[Session]" = weakref.WeakSet()  # closed by close()
 
     def close(self) -> None:
-        """Frees the live buffers and the context; raises the first error
-        after releasing everything."""
+        """Closes the live sessions, frees the live buffers and destroys the
+        context; every release runs even after an earlier one failed, and the
+        first error is raised afterwards."""
         if self.handle:
-            handle, self.handle = self.handle, None
             status = 0
+            for session in list(self._sessions):
+                rc = session._release()
+                status = status or rc
+            self._sessions.clear()
+            handle, self.handle = self.handle, None
             for b in self._buffers:
                 if b.ptr:
-                    status = status or _lib().ipus_buffer_free(handle, b.ptr)
+                    rc = _lib().ipus_buffer_free(handle, b.ptr)
+                    status = status or rc
                     b.ptr = 0
             self._buffers.clear()
-            status = status or _lib().ipus_context_destroy(handle)
+            rc = _lib().ipus_context_destroy(handle)
+            status = status or rc
             _check(status)
 
     def __enter__(self):
@@ -394,6 +406,19 @@ class Context:
             "global_memory_bytes": info.global_memory_bytes,
             "lds_bytes_per_block": info.lds_bytes_per_block,
         }
+
+    def live_buffers(self) -> tuple[int, int]:
+        """(count, bytes) of the buffers allocated through this context and
+        not yet freed, sessions' buffers included."""
+        n, b = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(_lib().ipus_context_live_buffers(self.handle, ctypes.byref(n), ctypes.byref(b)))
+        return n.value, b.value
+
+    def inject_launch_failure(self, launches_before: int, status: int) -> None:
+        """Test hook: the launch after `launches_before` more launches fails
+        with `status` (< 0) without running; 0 cancels."""
+        _check(_lib().ipus_context_inject_launch_failure(self.handle, int(launches_before),
+                                                         int(status)))
 
     def alloc(self, nbytes: int) -> DeviceBuffer:
         p = ctypes.c_void_p()
@@ -700,11 +725,18 @@ class Session:
         _check(_lib().ipus_session_create(context.handle, package.handle, ctypes.byref(h)))
         self.handle = h.value
         self._meta = {t.name: t for t in package.inputs + package.outputs}
+        context._sessions.add(self)
+
+    def _release(self) -> int:
+        """Destroys the C session once; returns its status (0 if already closed)."""
+        if not self.handle:
+            return 0
+        handle, self.handle = self.handle, None
+        self.context._sessions.discard(self)
+        return _lib().ipus_session_destroy(handle)
 
     def close(self) -> None:
-        if self.handle:
-            handle, self.handle = self.handle, None
-            _check(_lib().ipus_session_destroy(handle))
+        _check(self._release())
 
     def __del__(self):
         try:

@@ -125,6 +125,17 @@ uint64_t elements(const Shape& s) {
   return n;
 }
 
+// Product of every axis but the last `trailing` ones (the matrix or row
+// count).  Computed from the axes themselves, so a zero-extent matrix axis
+// leaves it well defined where elements / (rows * columns) would divide by 0.
+uint64_t outer_count(const Shape& s, size_t trailing) {
+  uint64_t n = 1;
+  for (size_t i = 0; i + trailing < s.size(); ++i) n *= s[i];
+  return n;
+}
+
+bool fits_u32(uint64_t v) { return v <= 0xffffffffull; }
+
 }  // namespace
 
 struct ipus_graph {
@@ -598,6 +609,7 @@ uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K, uint64_t batches, bool 
   const uint64_t b_span = tr ? 256ull * K * 2 : (uint64_t)K * N * 2;
   if (a_span >= (1ull << 31) || b_span >= (1ull << 31)) return 1;
   const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256) * batches;
+  if (tiles == 0) return 1;  // empty output: nothing to split
   const uint64_t want = std::min<uint64_t>({16, K / 1024, 64 / tiles});
   if (want < 2) return 1;
   const uint32_t chunk = (uint32_t)gemm_f16_split_chunk(K, (uint32_t)want);
@@ -634,6 +646,18 @@ struct Builder {
     pkg.steps.push_back(std::move(s));
   }
 
+  // An element-wise step over `count` elements as launches of at most
+  // kChunkElements each (the count scalar is u32; values of 2^32 elements
+  // and more fit in HBM).  Offsets advance by the elements already covered.
+  static constexpr uint64_t kChunkElements = 1ull << 30;
+  void emit_chunked(const std::string& symbol, int out, int in, uint64_t count,
+                    uint64_t in_bytes, uint64_t out_bytes) {
+    for (uint64_t done = 0; done < count; done += kChunkElements) {
+      const uint64_t n = std::min(kChunkElements, count - done);
+      emit(symbol, out, {{in, done * in_bytes}}, {(uint32_t)n}, done * out_bytes);
+    }
+  }
+
   // Returns a slot holding `slot`'s tensor as row-major with `precision`,
   // inserting Rearrange / Cast steps as needed (ensure_format, mid.rs:3553).
   int ensure(int slot, int precision) {
@@ -643,17 +667,20 @@ struct Builder {
       if (s.precision != IPUS_PRECISION_F16) return -1;
       const Shape& sh = s.shape;
       const uint32_t rows = sh[sh.size() - 2], cols = sh[sh.size() - 1];
-      const uint32_t matrices = (uint32_t)(elements(sh) / ((uint64_t)rows * cols));
+      const uint64_t matrices = outer_count(sh, 2);
+      if (!fits_u32(matrices)) return -1;
       const int out = new_slot(sh, s.precision);
       emit("ipu_stack_rearrange_to_row_major_f16", out, {{cur, 0}},
-           {(uint32_t)s.order, s.row_block, s.column_block, matrices, rows, cols});
+           {(uint32_t)s.order, s.row_block, s.column_block, (uint32_t)matrices, rows, cols});
       cur = out;
     }
     if (st(cur).precision != precision) {
       const int out = new_slot(st(cur).shape, precision);
-      const uint32_t n = (uint32_t)elements(st(cur).shape);
-      emit(precision == IPUS_PRECISION_F16 ? "ipu_stack_cast_f32_f16" : "ipu_stack_cast_f16_f32",
-           out, {{cur, 0}}, {n});
+      const uint64_t in_bytes = st(cur).precision == IPUS_PRECISION_F32 ? 4 : 2;
+      const uint64_t out_bytes = precision == IPUS_PRECISION_F32 ? 4 : 2;
+      emit_chunked(precision == IPUS_PRECISION_F16 ? "ipu_stack_cast_f32_f16"
+                                                   : "ipu_stack_cast_f16_f32",
+                   out, cur, elements(st(cur).shape), in_bytes, out_bytes);
       cur = out;
     }
     return cur;
@@ -686,10 +713,18 @@ struct Builder {
         const uint64_t batches = elements(ob);
         const char* sym = cp == IPUS_PRECISION_F32 ? "ipu_stack_gemm_f32" : "ipu_stack_gemm_f16";
         const uint64_t lcount = elements(lb), rcount = elements(rb);
+        // graph.rs broadcasts extents 0 and 1 to 1 (max), so an operand with
+        // an empty batch axis can meet a non-empty result: there is no data
+        // to read for it.
+        if (batches > 0 && (lcount == 0 || rcount == 0))
+          return build_error("GEMM operand with an empty batch axis broadcast to a non-empty result");
         // One launch when each operand is either fully batched or a single
         // matrix; otherwise one launch per output batch.
+        // The batch strides are u32 scalars: a batched operand whose matrix
+        // holds 2^32 elements or more takes the per-batch path below.
+        const bool strides_fit = (lcount == 1 || fits_u32(lm)) && (rcount == 1 || fits_u32(rm));
         if ((lcount == batches || lcount == 1) && (rcount == batches || rcount == 1) &&
-            batches <= 65535) {
+            batches <= 65535 && strides_fit) {
           if (cp == IPUS_PRECISION_F16) {
             const uint32_t splits = gemm_splits(M, N, K, batches, op.transpose_left,
                                                 op.transpose_right);
@@ -701,6 +736,8 @@ struct Builder {
                    {(uint32_t)batches, M, N, K, op.transpose_left ? 1u : 0u,
                     op.transpose_right ? 1u : 0u, (uint32_t)(lcount == 1 ? 0 : lm),
                     (uint32_t)(rcount == 1 ? 0 : rm), splits});
+              // At most 32 output tiles of 256 x 256 (gemm_splits), so the
+              // element count fits its u32 scalar.
               emit("ipu_stack_reduce_splits_f16", out, {{parts, 0}},
                    {splits, (uint32_t)(batches * M * N), 0u});
               return 0;
@@ -742,16 +779,12 @@ struct Builder {
         const int out = new_slot(s, IPUS_PRECISION_F16);
         env[op.results[0]] = out;
         const uint64_t n = elements(s);
-        if (n > 0xffffffffull) return build_error("GELU element count exceeds u32");
-        if (n % 2 == 0) {
-          emit("ipu_stack_gelu_tanh_approx_f16", out, {{in, 0}}, {(uint32_t)n});
-        } else {
-          // The reference ABI needs whole half pairs (kernel.rs:1400-1413):
-          // the even prefix goes through it, the last element through a
-          // one-element tail launch of the same kernel body.
-          if (n > 1) emit("ipu_stack_gelu_tanh_approx_f16", out, {{in, 0}}, {(uint32_t)(n - 1)});
-          emit("ipus_gelu_f16", out, {{in, (n - 1) * 2}}, {1u}, (n - 1) * 2);
-        }
+        // The reference ABI needs whole half pairs (kernel.rs:1400-1413):
+        // the even prefix goes through it (in launches of at most 2^30
+        // elements), an odd last element through a one-element tail launch
+        // of the same kernel body.
+        emit_chunked("ipu_stack_gelu_tanh_approx_f16", out, in, n - n % 2, 2, 2);
+        if (n % 2 == 1) emit("ipus_gelu_f16", out, {{in, (n - 1) * 2}}, {1u}, (n - 1) * 2);
         return 0;
       }
       case OpKind::Add: {
@@ -761,6 +794,8 @@ struct Builder {
         const int out = new_slot(os, cp);
         env[op.results[0]] = out;
         if (os.size() > 6) return build_error("Add supports rank <= 6");
+        if (elements(os) > 0 && (elements(st(l).shape) == 0 || elements(st(r).shape) == 0))
+          return build_error("Add operand with an empty axis broadcast to a non-empty result");
         std::vector<uint32_t> sc;
         sc.push_back((uint32_t)os.size());
         for (size_t i = 0; i < 6; ++i) sc.push_back(i < os.size() ? os[i] : 1);
@@ -771,7 +806,10 @@ struct Builder {
           for (int ax = (int)os.size() - 1; ax >= 0; --ax) {
             const int sa = ax - (int)(os.size() - s.size());
             if (sa >= 0) {
-              if (s[(size_t)sa] != 1) strides[(size_t)ax] = (uint32_t)stride;
+              if (s[(size_t)sa] != 1) {
+                if (!fits_u32(stride)) return build_error("Add operand strides exceed u32");
+                strides[(size_t)ax] = (uint32_t)stride;
+              }
               stride *= s[(size_t)sa];
             }
           }
@@ -800,12 +838,11 @@ struct Builder {
         if (q < 0 || k < 0 || v < 0) return build_error("attention operand format is not convertible");
         const Shape &qs = st(q).shape, &ks = st(k).shape, &vs = st(v).shape;
         const Shape& os = g.shapes.at(op.results[0]);
-        const uint64_t qstreams = elements(qs) / ((uint64_t)qs[qs.size() - 2] * qs.back());
-        const uint64_t kstreams = elements(ks) / ((uint64_t)ks[ks.size() - 2] * ks.back());
-        const uint64_t vstreams = elements(vs) / ((uint64_t)vs[vs.size() - 2] * vs.back());
-        const uint64_t ostreams = elements(os) / ((uint64_t)os[os.size() - 2] * os.back());
+        const uint64_t qstreams = outer_count(qs, 2), kstreams = outer_count(ks, 2);
+        const uint64_t vstreams = outer_count(vs, 2), ostreams = outer_count(os, 2);
         if (qstreams != ostreams || kstreams != ostreams || vstreams != ostreams)
           return build_error("attention batch broadcasting is not supported by the GPU plan");
+        if (!fits_u32(ostreams)) return build_error("attention stream count exceeds u32");
         const int prec = cfg.attention_output_f16 ? IPUS_PRECISION_F16 : IPUS_PRECISION_F32;
         const int out = new_slot(os, prec);
         env[op.results[0]] = out;
@@ -821,8 +858,9 @@ struct Builder {
         const uint32_t rows = s[s.size() - 2], cols = s[s.size() - 1];
         const int out = new_slot(g.shapes.at(op.results[0]), IPUS_PRECISION_F16);
         env[op.results[0]] = out;
-        emit("ipu_stack_transpose_f16", out, {{in, 0}},
-             {(uint32_t)(elements(s) / ((uint64_t)rows * cols)), rows, cols});
+        const uint64_t matrices = outer_count(s, 2);
+        if (!fits_u32(matrices)) return build_error("transpose matrix count exceeds u32");
+        emit("ipu_stack_transpose_f16", out, {{in, 0}}, {(uint32_t)matrices, rows, cols});
         return 0;
       }
       case OpKind::Rearrange: {
@@ -836,7 +874,9 @@ struct Builder {
         if (in < 0) return build_error("rearrange operand format is not convertible");
         const Shape& s = st(in).shape;
         const uint32_t rows = s[s.size() - 2], cols = s[s.size() - 1];
-        const uint32_t matrices = (uint32_t)(elements(s) / ((uint64_t)rows * cols));
+        const uint64_t matrices64 = outer_count(s, 2);
+        if (!fits_u32(matrices64)) return build_error("rearrange matrix count exceeds u32");
+        const uint32_t matrices = (uint32_t)matrices64;
         // Storage constraints (storage.rs:314-425): no padding at the graph
         // level, so the logical extents must fit the order's blocks.
         if (op.order == IPUS_ORDER_AMP_LEFT && cols % 16 != 0)
@@ -860,7 +900,8 @@ struct Builder {
         if (in < 0) return build_error("reduce_rows operand format is not convertible");
         const Storage& s = st(in);
         const uint64_t cols = s.shape.back();
-        const uint64_t rows = elements(s.shape) / (cols ? cols : 1);
+        const uint64_t rows = outer_count(s.shape, 1);
+        if (!fits_u32(rows)) return build_error("reduce_rows row count exceeds u32");
         const int out = new_slot(g.shapes.at(op.results[0]), IPUS_PRECISION_F32);
         env[op.results[0]] = out;
         emit("ipu_stack_reduce_rows_f16", out, {{in, 0}},
@@ -1064,7 +1105,7 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
     if (!reuse) {
       const Storage s = pkg->slots[(size_t)slot].storage;
       const int copy = b.new_slot(s.shape, s.precision, s.order, s.row_block, s.column_block);
-      b.emit("ipu_stack_copy", copy, {{slot, 0}}, {(uint32_t)s.bytes()});
+      b.emit_chunked("ipu_stack_copy", copy, slot, s.bytes(), 1, 1);
       slot = copy;
     }
     pkg->slots[(size_t)slot].external = true;

@@ -8,9 +8,20 @@
 
 #include "../../include/ipus.h"
 
+#include <mutex>
+#include <unordered_map>
+
 struct ipus_context {
   int device = 0;
   hipStream_t stream = nullptr;
+  // Buffers allocated through this context and not yet freed (pointer ->
+  // bytes); ipus_context_destroy releases whatever is left.
+  std::mutex live_mutex;
+  std::unordered_map<void*, size_t> live;
+  // Failure injection (ipus_context_inject_launch_failure): after
+  // inject_after more launches, the next one returns inject_status.
+  uint32_t inject_after = 0;
+  int inject_status = 0;
 };
 
 namespace ipus {

@@ -38,12 +38,11 @@
 //     runs with streaming stores (8192^3: +4%; 4096 x 16384 x 4096: +17%);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
 //     dispatch over 8 XCDs) form a compact group of C tiles sharing L2;
-//   * partial tiles: rows of a K-contiguous operand past M or N, and rows of
-//     an MN-contiguous one past K, lie past the buffer's range and read as
-//     0; MN-contiguous chunks past M or N, and (in the KTail instantiation,
-//     K % 64 != 0) K-contiguous chunks past K on the last step, get an
-//     offset past the range; the epilogue stores only rows < M and 8-column
-//     chunks < N.
+//   * partial tiles: rows of a K-contiguous operand past M or N lie past
+//     the buffer's range and read as 0; MN-contiguous chunks past M or N,
+//     and (in the KTail instantiation, K % 64 != 0) K-contiguous chunks and
+//     MN-contiguous rows past K on the last step, get an offset past the
+//     range; the epilogue stores only rows < M and 8-column chunks < N.
 // General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
 #include "../../include/ipus.h"
 #include "device_common.h"
@@ -118,8 +117,8 @@ __device__ __forceinline__ void tile_offsets(uint32_t wave, uint32_t lane, uint3
       const uint32_t k = inst * 2 + lane / 32;  // 2 rows of 512 bytes
       const uint32_t phys = lane % 32;
       const uint32_t chunk = (mc_off(k, phys) - k * 512u) >> 4;
-      // mn_limit: columns of this tile inside the operand (rows past K are
-      // past the buffer's range already).
+      // mn_limit: columns of this tile inside the operand (rows past K, on
+      // the last step only, are masked by issue_tile_mn_tail).
       voff[j] = chunk * 8 < mn_limit ? (k * ld + chunk * 8) * 2 : kPadOffset;
     }
   }
@@ -146,6 +145,24 @@ __device__ __forceinline__ void issue_tile_k_tail(__amdgpu_buffer_rsrc_t rsrc, u
     const uint32_t chunk = (kc_off<BK>(row, lane % kChunks) - row * (BK * 2)) >> 4;
     dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024,
           chunk * 8 < k_limit ? voff[j] : kPadOffset, soffset);
+  }
+}
+
+// The last K step of an MN-contiguous operand when K % BK != 0: tile rows k
+// at or past k_limit get an offset past the range and read 0.  The step's K
+// offset travels in the scalar offset, which the descriptor's range check
+// does not cover, so rows past K cannot be left to the range of the vector
+// offset alone: they would read the memory after the operand.
+template <int BK>
+__device__ __forceinline__ void issue_tile_mn_tail(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
+                                                   uint32_t wave, uint32_t lane,
+                                                   const uint32_t* voff, uint32_t soffset,
+                                                   uint32_t k_limit) {
+#pragma unroll
+  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
+    const uint32_t k = (wave * Tile<BK>::kDmaPerWave + j) * 2 + lane / 32;  // as tile_offsets
+    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024,
+          k < k_limit ? voff[j] : kPadOffset, soffset);
   }
 }
 
@@ -242,15 +259,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   // KTail (K % BK != 0) is a separate instantiation, so the branch never
   // enters the scheduled K loop of the common case.
   auto issue_a = [&](uint8_t* ta, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && kAK && k_tail != 0 && k == ksteps - 1)
-      issue_tile_k_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
-    else
+    if (KTail && k_tail != 0 && k == ksteps - 1) {
+      if constexpr (kAK)
+        issue_tile_k_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
+      else
+        issue_tile_mn_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
+    } else
       issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
   };
   auto issue_b = [&](uint8_t* tb, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && kBK_ && k_tail != 0 && k == ksteps - 1)
-      issue_tile_k_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
-    else
+    if (KTail && k_tail != 0 && k == ksteps - 1) {
+      if constexpr (kBK_)
+        issue_tile_k_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
+      else
+        issue_tile_mn_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
+    } else
       issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
   };
   auto fetch = [&](uint8_t* ta, uint8_t* tb, uint32_t k) {

@@ -117,6 +117,11 @@ extern "C" int ipus_context_destroy(ipus_context* ctx) {
   if (e != hipSuccess && status == 0) status = hip_fail(e, "hipStreamSynchronize");
   e = hipStreamDestroy(ctx->stream);
   if (e != hipSuccess && status == 0) status = hip_fail(e, "hipStreamDestroy");
+  // Buffers the caller did not free are released with the context.
+  for (const auto& kv : ctx->live) {
+    e = hipFree(kv.first);
+    if (e != hipSuccess && status == 0) status = hip_fail(e, "hipFree");
+  }
   delete ctx;
   return status;
 }
@@ -155,15 +160,43 @@ extern "C" int ipus_buffer_alloc(ipus_context* ctx, size_t bytes, void** ptr) {
   if (e == hipErrorOutOfMemory)
     return fail(IPUS_ERROR_OUT_OF_MEMORY, "out of device memory allocating %zu bytes", bytes);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  std::lock_guard<std::mutex> lock(ctx->live_mutex);
+  ctx->live[*ptr] = bytes;
   return 0;
 }
 
 extern "C" int ipus_buffer_free(ipus_context* ctx, void* ptr) {
   if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
   if (!ptr) return 0;
+  {
+    std::lock_guard<std::mutex> lock(ctx->live_mutex);
+    auto it = ctx->live.find(ptr);
+    if (it == ctx->live.end())
+      return fail(IPUS_ERROR_INVALID_ARGUMENT, "%p is not a live buffer of this context", ptr);
+    ctx->live.erase(it);
+  }
   if (int e = use_device(ctx)) return e;
   hipError_t e = hipFree(ptr);
   if (e != hipSuccess) return hip_fail(e, "hipFree");
+  return 0;
+}
+
+extern "C" int ipus_context_live_buffers(ipus_context* ctx, uint64_t* count, uint64_t* bytes) {
+  if (!ctx || !count || !bytes) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  std::lock_guard<std::mutex> lock(ctx->live_mutex);
+  *count = ctx->live.size();
+  uint64_t total = 0;
+  for (const auto& kv : ctx->live) total += kv.second;
+  *bytes = total;
+  return 0;
+}
+
+extern "C" int ipus_context_inject_launch_failure(ipus_context* ctx, uint32_t launches_before,
+                                                  int status) {
+  if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
+  if (status > 0) return fail(IPUS_ERROR_INVALID_ARGUMENT, "injected status must be <= 0");
+  ctx->inject_after = launches_before;
+  ctx->inject_status = status;
   return 0;
 }
 
@@ -600,6 +633,14 @@ extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
     if (!inputs || !inputs[k])
       return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null input %d", symbol, k);
   if (scalar_count && !scalars) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null scalars");
+  if (ctx->inject_status != 0) {
+    if (ctx->inject_after == 0) {
+      const int status = ctx->inject_status;
+      ctx->inject_status = 0;
+      return fail(status, "kernel %s: injected launch failure (%d)", symbol, status);
+    }
+    --ctx->inject_after;
+  }
   if (int e = use_device(ctx)) return e;
   return check_launch(e->launch(ctx, output, inputs, scalars), symbol);
 }

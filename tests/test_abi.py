@@ -106,3 +106,13 @@ def test_synth_is_deterministic_and_matches_splitmix(ipus, oracle):
         assert a[i] == oracle.f32_to_f16(np.array([expect]))[0]
     n = ipus.synth_f32(1 << 16, 5, 1, ipus.NORMAL)
     assert abs(float(n.mean())) < 0.02 and abs(float(n.std()) - 1.0) < 0.02
+
+
+def test_failure_injection_and_live_buffer_calls_validate_arguments(ipus):
+    """The test hooks exist in the C ABI and reject a null context on the CPU
+    (their GPU behaviour is covered by the package tests)."""
+    lib = ipus._lib()
+    assert lib.ipus_context_inject_launch_failure(None, 0, -1) == ipus.ERROR_INVALID_ARGUMENT
+    n = ipus.ctypes.c_uint64()
+    assert lib.ipus_context_live_buffers(None, ipus.ctypes.byref(n), ipus.ctypes.byref(n)) == \
+        ipus.ERROR_INVALID_ARGUMENT

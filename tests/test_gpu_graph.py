@@ -268,3 +268,95 @@ def test_captured_session_replays_match_eager(ipus, ctx, which):
     finally:
         eager.close()
         graph.close()
+
+
+def test_mlp_package_full_size_configs3(ipus, oracle, ctx):
+    """BASELINE configs[3] at its full size: X[4096, 4096] ~ N(0, 1),
+    W1[4096, 16384] and W2[16384, 4096] ~ N(0, 0.02), X . W1 -> GELU -> . W2.
+    Row i of Y depends only on row i of X, so 24 sampled rows (every stream
+    of 256-row tiles, both edges) are checked against the oracle:
+    y_i = f16(f16(gelu(f16(x_i . W1))) . W2)."""
+    m, d, h = 4096, 4096, 16384
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [m, d])
+    w1 = g.parameter("w1", [d, h])
+    w2 = g.parameter("w2", [h, d])
+    g.set_outputs([g.gemm(g.gelu(g.gemm(x, w1)), w2)])
+    xs = synth(ipus, m * d, 2024, 1)
+    w1s = synth(ipus, d * h, 2024, 2, scale=0.02)
+    w2s = synth(ipus, h * d, 2024, 3, scale=0.02)
+    pkg, (y,) = run_package(ipus, ctx, g, {"x": xs.reshape(m, d), "w1": w1s.reshape(d, h),
+                                          "w2": w2s.reshape(h, d)})
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16"]
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, m - 1],
+                                     np.linspace(2, m - 2, 19).astype(np.int64)]))
+    xr = xs.reshape(m, d)[rows]
+    hidden = oracle.gelu_f16(oracle.f32_to_f16(
+        oracle.gemm_f16_rows(xr, w1s, len(rows), h, d, np.arange(len(rows)))))
+    want = oracle.f16_to_f32(oracle.f32_to_f16(
+        oracle.gemm_f16_rows(hidden, w2s, len(rows), d, h, np.arange(len(rows)))))
+    got = oracle.f16_to_f32(y.reshape(m, d)[rows])
+    assert np.all(np.isfinite(got))
+    assert fp16_close(got, want, FP16_TOL), max_rel(got, want)
+
+
+def test_injected_launch_failure_propagates_and_releases_everything(ipus, oracle, ctx):
+    """A launch that fails inside ipus_session_run or ipus_session_capture
+    surfaces as that call's error (the first failing step's status and
+    message), leaves the stream usable, and every buffer is released by
+    session and context teardown (the role of the reference's failure path,
+    crates/ipu-tests/src/main.rs:985-1006; the failure is injected on the
+    host, so no kernel faults)."""
+    status = -1000 - 700  # IPUS_ERROR_HIP_BASE - hipErrorIllegalAddress
+    base = ctx.live_buffers()
+    m, d, h = 128, 128, 512
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [m, d])
+    w1 = g.parameter("w1", [d, h])
+    w2 = g.parameter("w2", [h, d])
+    g.set_outputs([g.add(g.gemm(g.gelu(g.gemm(x, w1)), w2), x)])
+    pkg = ipus.build_package(g)
+    assert len(pkg.steps) == 3
+    feeds = {"x": synth(ipus, m * d, 51, 1).reshape(m, d),
+             "w1": synth(ipus, d * h, 51, 2, scale=0.05).reshape(d, h),
+             "w2": synth(ipus, h * d, 51, 3, scale=0.05).reshape(h, d)}
+    sess = pkg.session(ctx)
+    assert ctx.live_buffers()[0] > base[0]
+    for name, array in feeds.items():
+        sess.write(name, array)
+    sess.run_sync()
+    want = sess.read("output.0")
+    # Eager run: the second step fails; nothing after it runs.
+    ctx.inject_launch_failure(1, status)
+    with pytest.raises(ipus.IpusError) as err:
+        sess.run()
+    assert err.value.status == status and "injected" in err.value.message
+    ctx.sync()
+    sess.run_sync()
+    assert np.array_equal(sess.read("output.0"), want)
+    # Capture: the failing launch ends the capture with the error and no
+    # graph; eager runs and a later capture work.
+    ctx.inject_launch_failure(0, status)
+    with pytest.raises(ipus.IpusError) as err:
+        sess.capture()
+    assert err.value.status == status
+    sess.run_sync()
+    assert np.array_equal(sess.read("output.0"), want)
+    sess.capture()
+    for _ in range(2):
+        sess.run_sync()
+        assert np.array_equal(sess.read("output.0"), want)
+    sess.close()
+    assert ctx.live_buffers() == base
+    # Context.close with a session still open after a failure releases the
+    # session, its buffers and the context.
+    c2 = ipus.Context(0)
+    s2 = pkg.session(c2)
+    extra = c2.alloc(4096)
+    c2.inject_launch_failure(0, status)
+    with pytest.raises(ipus.IpusError):
+        s2.run()
+    c2.close()
+    assert s2.handle is None and extra.ptr == 0
+    with pytest.raises(ipus.IpusError):
+        s2.run()

@@ -504,3 +504,113 @@ def test_gemm_empty_inner_dimension_is_zero(ipus, ctx, symbol, elem):
     assert not np.any(got)
     for b in (out, src):
         b.free()
+
+
+# ---------------------------------------------------------------------------
+# Cast (kernel.rs:1313-1318) and flat Add (kernel.rs:1275-1287)
+# ---------------------------------------------------------------------------
+def _same_or_both_nan(got_f, want_f, got_bits, want_bits):
+    nan = np.isnan(want_f)
+    assert np.array_equal(np.isnan(got_f), nan)
+    assert np.array_equal(got_bits[~nan], want_bits[~nan])
+
+
+def test_cast_f16_f32_every_pattern(ipus, oracle, ctx):
+    """All 65536 fp16 patterns widen exactly (binary16 -> binary32 is exact;
+    NaNs stay NaN)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = run(ctx, "ipu_stack_cast_f16_f32", bits.size * 4, [bits], [bits.size], np.float32)
+    want = oracle.f16_to_f32(bits)
+    _same_or_both_nan(got, want, got.view(np.uint32), want.view(np.uint32))
+
+
+def test_cast_f32_f16_round_to_nearest_even(ipus, oracle, ctx):
+    """fp32 -> fp16 rounds to nearest even (half 2.7.1, main.rs:2040-2046):
+    every fp16 value exactly, the midpoints between neighbours (ties), values
+    just either side of them, fp16 overflow (65504 .. 65520 .. inf),
+    fp16 subnormals and their ties, fp32 subnormals, signed zeros, inf, NaN
+    and random fp32 over the whole exponent range."""
+    f16 = oracle.f16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    finite = np.unique(f16[np.isfinite(f16)]).astype(np.float64)
+    mids = ((finite[:-1] + finite[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    down = np.nextafter(mids, np.float32(-np.inf))
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65519.996, 65520.0,
+                        65535.0, 1e6, -65520.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                        2.0 ** -26, 1e-40, -1e-40, 1.4e-45, 6.1e-5, 6.0e-5],
+                       dtype=np.float32)
+    rng = np.random.default_rng(5)
+    rand = (rng.standard_normal(200000) * np.exp2(rng.uniform(-30, 20, 200000))).astype(np.float32)
+    x = np.concatenate([f16, mids, up, down, special, rand]).astype(np.float32)
+    got = run(ctx, "ipu_stack_cast_f32_f16", x.size * 2, [x], [x.size])
+    want = oracle.f32_to_f16(x)
+    _same_or_both_nan(oracle.f16_to_f32(got), oracle.f16_to_f32(want), got, want)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("count,L,R", [
+    (4096, 4096, 4096),      # no broadcast
+    (6144, 6144, 1024),      # right repeats (L > R)
+    (6144, 1536, 6144),      # left repeats (L < R)
+    (1000, 1, 1000),         # scalar left
+    (999, 999, 1),           # scalar right
+    (1 << 20, 4096, 64),     # both repeat with different periods
+])
+def test_flat_add_broadcast_strides(ipus, oracle, ctx, dtype, count, L, R):
+    """out[i] = left[i % L] + right[i % R]; fp16 as the fp32 sum rounded once
+    (diagnostic.rs:673-683, 841-847), bit-exact."""
+    rng = np.random.default_rng(count + L + R)
+    lf = rng.standard_normal(L).astype(np.float32)
+    rf = rng.standard_normal(R).astype(np.float32)
+    i = np.arange(count)
+    if dtype == "f16":
+        lb, rb = oracle.f32_to_f16(lf), oracle.f32_to_f16(rf)
+        want = oracle.f32_to_f16(oracle.f16_to_f32(lb)[i % L] + oracle.f16_to_f32(rb)[i % R])
+        got = run(ctx, "ipu_stack_add_f16", count * 2, [lb, rb], [count, L, R])
+        assert np.array_equal(got, want)
+    else:
+        want = (lf[i % L] + rf[i % R]).astype(np.float32)
+        # The oracle's broadcasting add agrees where the flat form is a
+        # numpy broadcast ([count / max, max] against [max] or [min]).
+        if L == count and count % R == 0:
+            ref = oracle.add_f32(lf.reshape(-1, R), rf).reshape(-1)
+            assert np.array_equal(ref, want)
+        got = run(ctx, "ipu_stack_add_f32", count * 4, [lf, rf], [count, L, R], np.float32)
+        assert np.array_equal(got, want)
+
+
+def test_flat_add_rejects_strides_that_do_not_divide(ipus, ctx):
+    buf = ctx.alloc(64)
+    for scalars in ([16, 3, 16], [16, 16, 0], [16, 8, 12]):
+        with pytest.raises(ipus.IpusError):
+            ctx.launch("ipu_stack_add_f16", buf, [buf, buf], scalars)
+    buf.free()
+
+
+# ---------------------------------------------------------------------------
+# GEMM K tail: reads past K stay inside the operand
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,tl,tr", [
+    (729, 1152, 4304, 0, 0),   # NN, K % 64 = 16: row-major B is MN-contiguous
+    (264, 520, 72, 1, 0),      # A^T and B both MN-contiguous, K % 64 = 8
+    (264, 520, 72, 0, 1),      # both K-contiguous
+    (130, 264, 200, 1, 1),     # A^T MN-contiguous, B^T K-contiguous
+])
+def test_gemm_k_tail_ignores_memory_after_the_operands(ipus, oracle, ctx, M, N, K, tl, tr):
+    """Each operand is followed in its own allocation by 64 rows of fp16 NaN:
+    a K-tail load that read past K (rather than the masked zero) would turn
+    the product NaN."""
+    nan = np.uint16(0x7E00)
+    a = synth(ipus, M * K, 41, 1)
+    b = synth(ipus, K * N, 41, 2)
+    pad = 64 * max(M, N, K) + 64
+    da = ctx.upload(np.concatenate([a, np.full(pad, nan, np.uint16)]))
+    db = ctx.upload(np.concatenate([b, np.full(pad, nan, np.uint16)]))
+    out = ctx.alloc(M * N * 2)
+    ctx.launch("ipu_stack_gemm_f16", out, [da, db], [1, M, N, K, tl, tr, 0, 0])
+    got = oracle.f16_to_f32(out.download(np.uint16))
+    assert not np.any(np.isnan(got))
+    want = oracle.f16_to_f32(oracle.gemm_f16(a, b, M, N, K, bool(tl), bool(tr)))
+    assert fp16_close(got, want, FP16_TOL)
+    for x in (da, db, out):
+        x.free()

@@ -5,6 +5,7 @@ The randomized shape tests restate crates/ipu-codegen/src/graph.rs:806-966
 (graph.rs:221-245)."""
 from __future__ import annotations
 
+import math
 import random
 
 import pytest
@@ -368,3 +369,84 @@ def test_build_package_f32_compute(ipus):
     pkg = ipus.build_package(g, ipus.PackageConfig(compute_precision="f32"))
     assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f32"]
     assert pkg.inputs[0].precision == ipus.PRECISION_F32
+
+
+@pytest.mark.parametrize("build", [
+    lambda ipus, g: g.gemm(g.host_input("x", [0, 4096]), g.parameter("w", [4096, 256])),
+    lambda ipus, g: g.gemm(g.host_input("x", [256, 4096]), g.parameter("w", [4096, 0])),
+    lambda ipus, g: g.gemm(g.host_input("x", [0, 256, 4096]), g.parameter("w", [0, 4096, 256])),
+    lambda ipus, g: g.gemm(g.host_input("x", [256, 0]), g.parameter("w", [0, 256])),
+    lambda ipus, g: g.transpose(g.host_input("x", [0, 64])),
+    lambda ipus, g: g.transpose(g.host_input("x", [3, 64, 0])),
+    lambda ipus, g: g.rearrange(g.host_input("x", [0, 64]), ipus.ORDER_BLOCK_MAJOR, 64, 64),
+    lambda ipus, g: g.reduce_rows(g.host_input("x", [64, 0])),
+    lambda ipus, g: g.reduce_rows(g.host_input("x", [0, 64])),
+    lambda ipus, g: g.gelu(g.host_input("x", [0, 7])),
+    lambda ipus, g: g.flash_attention(g.host_input("q", [2, 0, 64]), g.host_input("k", [2, 5, 64]),
+                                      g.host_input("v", [2, 5, 64])),
+    lambda ipus, g: g.flash_attention(g.host_input("q", [2, 5, 64]), g.host_input("k", [2, 0, 64]),
+                                      g.host_input("v", [2, 0, 64])),
+])
+def test_build_package_zero_extents(ipus, build):
+    """Zero extents are legal graph values (graph.rs shape inference accepts
+    them); the plan must build without dividing by a zero matrix size."""
+    g = ipus.ComputeGraph()
+    g.set_outputs([build(ipus, g)])
+    pkg = ipus.build_package(g)
+    out = pkg.outputs[0]
+    assert out.nbytes == math.prod(out.shape) * (4 if out.precision == ipus.PRECISION_F32 else 2)
+    for symbol, _inputs, scalars in pkg.steps:
+        assert all(0 <= s <= 0xFFFFFFFF for s in scalars), symbol
+
+
+def test_build_package_rejects_empty_batch_broadcast_to_one(ipus):
+    """graph.rs:755-777 broadcasts extents 0 and 1 to 1 (the larger), so a
+    GEMM or Add result can be non-empty while an operand holds no data: the
+    plan refuses instead of reading past an empty buffer."""
+    g = ipus.ComputeGraph()
+    out = g.gemm(g.host_input("x", [0, 256, 64]), g.parameter("w", [64, 256]))
+    assert g.value_shape(out) == (1, 256, 256)
+    g.set_outputs([out])
+    with pytest.raises(ipus.PackageBuildError):
+        ipus.build_package(g)
+    g = ipus.ComputeGraph()
+    out = g.add(g.host_input("x", [0, 8]), g.host_input("y", [1, 8]))
+    assert g.value_shape(out) == (1, 8)
+    g.set_outputs([out])
+    with pytest.raises(ipus.PackageBuildError):
+        ipus.build_package(g)
+
+
+def test_build_package_splits_u32_element_counts(ipus):
+    """Values of 2^32 elements and more fit in HBM: element-wise steps whose
+    count scalar would overflow u32 are split into launches of at most 2^30
+    elements instead of being truncated."""
+    shape = [65536, 65538]
+    n = 65536 * 65538                       # 2^32 + 2^17 elements
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", shape)
+    g.set_outputs([g.gelu(x), x])
+    pkg = ipus.build_package(g)
+    gelu = [s for s in pkg.steps if s[0] == "ipu_stack_gelu_tanh_approx_f16"]
+    assert [s[2][0] for s in gelu] == [1 << 30] * 4 + [1 << 17]
+    copies = [s for s in pkg.steps if s[0] == "ipu_stack_copy"]
+    assert sum(s[2][0] for s in copies) == 2 * n and max(s[2][0] for s in copies) == 1 << 30
+    # An fp32 graph value of 2^32 + 2^17 elements cast for GELU (F32 compute).
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", shape)
+    g.set_outputs([g.gelu(x)])
+    pkg = ipus.build_package(g, ipus.PackageConfig(compute_precision="f32"))
+    casts = [s for s in pkg.steps if s[0] == "ipu_stack_cast_f32_f16"]
+    assert sum(s[2][0] for s in casts) == n and len(casts) == 5
+
+
+def test_build_package_batched_gemm_with_u32_overflowing_stride(ipus):
+    """A batched operand whose matrix holds 2^32 elements or more cannot pass
+    its batch stride as a u32 scalar: the plan launches per batch."""
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [2, 65536, 65544])
+    w = g.parameter("w", [65544, 8])
+    g.set_outputs([g.gemm(x, w)])
+    pkg = ipus.build_package(g)
+    gemms = [s for s in pkg.steps if s[0] == "ipu_stack_gemm_f16"]
+    assert len(gemms) == 2 and all(s[2][0] == 1 and s[2][6] == 0 for s in gemms)

@@ -107,6 +107,60 @@ def test_unpack_sources_match_unpack_cpp(oracle):
             assert oracle.amp_matrix_index(oracle.AMP_TRANSPOSED_LEFT, oracle.F16, PR, PC, r, c) == tl
 
 
+def _unpack_vertex(source_order, matrices, lr, pr, lc, pc, source):
+    """device/unpack_amp_f16.cpp:40-80 restated word for word: a pass over the
+    physical rows of every matrix writes 32-bit words of two fp16 columns at
+    matrixBase + row * physicalColumns + column; a word whose row or first
+    column lies past the logical extent is 0, and so is a second lane past
+    the logical columns.  Source and destination share matrixBase =
+    matrix * physicalRows * physicalColumns."""
+    words = source.astype(np.uint32)
+    out = np.full(matrices * pr * pc // 2, 0xDEADBEEF, dtype=np.uint32)
+    matrix_elements = pr * pc
+    for matrix_row in range(matrices * pr):
+        matrix, row = divmod(matrix_row, pr)
+        base = matrix * matrix_elements
+        for column in range(0, pc, 2):
+            packed = 0
+            if row < lr and column < lc:
+                for lane in range(2):
+                    c = column + lane
+                    if c >= lc:
+                        continue
+                    if source_order == 0:
+                        logical_pair = c % 16 // 2
+                        physical_pair = logical_pair % 4 * 2 + logical_pair // 4
+                        physical = (c // 16) * pr * 16 + row * 16 + physical_pair * 2 + c % 2
+                    else:
+                        physical = (row // 16) * pc * 16 + c * 16 + row % 16
+                    packed |= int(words[base + physical]) << (lane * 16)
+            out[(base + row * pc + column) // 2] = packed
+    return out.view(np.uint16)
+
+
+@pytest.mark.parametrize("source_order", [0, 1])
+@pytest.mark.parametrize("matrices,lr,pr,lc,pc", [
+    (1, 16, 16, 16, 16),    # one micro-panel, no padding
+    (2, 30, 32, 40, 48),    # padding on both axes, two matrices
+    (3, 17, 32, 33, 48),    # odd logical columns: a word with one real lane
+    (2, 32, 32, 31, 32),    # column padding only
+    (1, 5, 16, 64, 64),     # row padding only, four column panels
+])
+def test_unpack_to_row_major_matches_unpack_vertex(oracle, source_order, matrices, lr, pr, lc,
+                                                   pc):
+    """Pins or_unpack_to_row_major_f16's matrix base, destination pitch and zero
+    padding against the vertex loop, with a source whose every element is
+    distinct and nonzero (so a wrong base, pitch or pad rule shows)."""
+    src = (np.arange(matrices * pr * pc, dtype=np.uint32) % 65535 + 1).astype(np.uint16)
+    want = _unpack_vertex(source_order, matrices, lr, pr, lc, pc, src)
+    got = oracle.unpack_to_row_major_f16(src, source_order, matrices, lr, pr, lc, pc)
+    assert np.array_equal(got, want)
+    # Padding is zero and every logical element appears once.
+    got3 = got.reshape(matrices, pr, pc)
+    assert not np.any(got3[:, lr:, :]) and not np.any(got3[:, :, lc:])
+    assert np.unique(got3[:, :lr, :lc]).size == matrices * lr * lc
+
+
 def test_amp_output_pair_permutation_matches_gelu_reorder_table(oracle):
     """crates/ipu-tests/src/diagnostic.rs:910-946: AMP-Output word s of a
     16-column group holds the logical pair permutation[s] of AMP-Left."""
