@@ -212,6 +212,28 @@ int ipus_launch(ipus_context *context, const char *symbol, void *output,
                 const void *const *inputs, int input_count, const uint32_t *scalars,
                 int scalar_count);
 
+/* ---- split-K fp16 GEMM that allocates nothing ----
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same computation as launching
+ * ipu_stack_gemm_f16_split into a caller-allocated partials buffer and then
+ * ipu_stack_reduce_splits_f16 (gelu 0/1) into `output`, with the partials in
+ * a device array the library holds for each device from its first context
+ * until the process ends.  Arguments are those two symbols' scalars; the
+ * operands and output follow ipu_stack_gemm_f16.  The partials,
+ * batches * rows * columns * splits fp32 values, must fit
+ * IPUS_SPLIT_SCRATCH_BYTES (16 MiB: build_package's split plans, at most 64
+ * split tiles of 256 x 256, all fit), else IPUS_ERROR_UNSUPPORTED_COUNT.
+ * The call enqueues on the context's stream and calls no allocator.  Every
+ * call on one device shares that device's array: calls that overlap on one
+ * device (from different streams or threads) race. */
+#define IPUS_SPLIT_SCRATCH_BYTES (16ull << 20)
+int ipus_gemm_f16_split_noalloc(ipus_context *context, void *output, const void *left,
+                                const void *right, uint32_t batches, uint32_t rows,
+                                uint32_t columns, uint32_t inner, int transpose_left,
+                                int transpose_right, uint64_t left_batch_stride,
+                                uint64_t right_batch_stride, uint32_t splits, int gelu);
+
 /* ---- synthetic inputs (host, deterministic, multithreaded) ----
  * value(seed, tensor, i) from SplitMix64(seed ^ (tensor << 48) ^ i):
  * distribution 0 = uniform [-1, 1) from the top 24 bits, 1 = normal (Box-Muller

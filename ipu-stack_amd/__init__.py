@@ -128,6 +128,10 @@ _SIGNATURES = {
     "ipus_context_live_buffers": (
         ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "ipus_context_inject_launch_failure": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_int]),
+    "ipus_gemm_f16_split_noalloc": (
+        ctypes.c_int, [_P, _P, _P, _P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                       ctypes.c_uint32, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
+                       ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int]),
     "ipus_buffer_upload": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
     "ipus_buffer_download": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
     "ipus_buffer_copy": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
@@ -462,6 +466,18 @@ class Context:
         sc, n = _u32_array(scalars)
         outp = out.ptr if isinstance(out, DeviceBuffer) else int(out)
         _check(_lib().ipus_launch(self.handle, symbol.encode(), outp, in_arr, len(ptrs), sc, n))
+
+    def gemm_f16_split_noalloc(self, out, left, right, batches, rows, columns, inner,
+                               transpose_left=False, transpose_right=False,
+                               left_batch_stride=0, right_batch_stride=0, splits=2,
+                               gelu=False) -> None:
+        """Split-K fp16 GEMM whose partials use the library's per-device
+        scratch array (ipus_gemm_f16_split_noalloc): no allocation."""
+        ptr = lambda x: x.ptr if isinstance(x, DeviceBuffer) else int(x)  # noqa: E731
+        _check(_lib().ipus_gemm_f16_split_noalloc(
+            self.handle, ptr(out), ptr(left), ptr(right), int(batches), int(rows), int(columns),
+            int(inner), int(bool(transpose_left)), int(bool(transpose_right)),
+            int(left_batch_stride), int(right_batch_stride), int(splits), int(bool(gelu))))
 
     def timer(self) -> "Timer":
         return Timer(self)

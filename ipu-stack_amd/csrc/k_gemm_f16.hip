@@ -45,6 +45,9 @@
 //     range; the epilogue stores only rows < M and 8-column chunks < N.
 // General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
 #include "../../include/ipus.h"
+
+#include <mutex>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -595,6 +598,56 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
                      a.rows, a.columns, a.inner, a.transpose_left, a.transpose_right,
                      a.left_batch_stride, a.right_batch_stride, tiles_n, a.gelu);
   return hip_status(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Split-K without allocation (ipus_gemm_f16_split_noalloc): the fp32
+// partials go to `scratch`, a file-scope device array of
+// IPUS_SPLIT_SCRATCH_BYTES that each device holds from module load until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol): split_scratch_init looks up
+// each device's copy once, with that device current, and the launches take
+// the looked-up pointer.  Every split writes its whole partial tile, so
+// nothing in the array has to start at zero.  All calls on one device share
+// its array: calls that overlap on one device (different streams) race.
+// ---------------------------------------------------------------------------
+namespace {
+static __device__ __align__(256) float scratch[IPUS_SPLIT_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+int split_scratch_init(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return IPUS_ERROR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device]) return 0;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_status(e);
+  if (!ptr) return IPUS_ERROR_INVALID_ARGUMENT;
+  g_scratch_ptr[device] = ptr;
+  return 0;
+}
+
+int launch_gemm_f16_split_noalloc(hipStream_t stream, int device, const GemmArgs& a,
+                                  uint32_t splits) {
+  if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
+  void* parts = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (device >= 0 && device < kMaxScratchDevices) parts = g_scratch_ptr[device];
+  }
+  if (!parts) return IPUS_ERROR_NO_DEVICE;
+  const uint64_t count = (uint64_t)a.batches * a.rows * a.columns;
+  if (splits == 0 || count * splits > IPUS_SPLIT_SCRATCH_BYTES / sizeof(float))
+    return IPUS_ERROR_UNSUPPORTED_COUNT;
+  GemmArgs s = a;
+  s.out = parts;
+  s.gelu = false;
+  if (int e = launch_gemm_f16_split(stream, s, splits)) return e;
+  return launch_reduce_splits_f16(stream, a.out, parts, splits, count, a.gelu);
 }
 
 }  // namespace ipus

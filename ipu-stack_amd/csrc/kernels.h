@@ -45,6 +45,14 @@ int gemm_f16_split_chunk(uint32_t inner, uint32_t splits);
 int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits);
 int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
                              uint64_t count, bool gelu);
+// Split-K with the partials in the library's per-device scratch array
+// (no allocation): split_scratch_init(device) looks up the device's copy
+// once, with that device current; the launch then runs the split GEMM into
+// it and the reduction into a.out (GELU when a.gelu).  Partials beyond
+// IPUS_SPLIT_SCRATCH_BYTES return IPUS_ERROR_UNSUPPORTED_COUNT.
+int split_scratch_init(int device);
+int launch_gemm_f16_split_noalloc(hipStream_t stream, int device, const GemmArgs& a,
+                                  uint32_t splits);
 int launch_gemm_f32(hipStream_t stream, const GemmArgs& a);
 
 // Fused online-softmax attention (k_attention.hip).

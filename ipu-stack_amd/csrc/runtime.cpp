@@ -104,6 +104,14 @@ extern "C" int ipus_context_create(int device, ipus_context** out) {
     delete ctx;
     return hip_fail(e, "hipStreamCreate");
   }
+  // Per-device address of the no-allocation entry point's scratch array,
+  // looked up once per device with that device current.
+  if (int status = split_scratch_init(device)) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return fail(status, "device %d: looking up the split-K scratch array failed (%d)", device,
+                status);
+  }
   *out = ctx;
   return 0;
 }
@@ -643,6 +651,38 @@ extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
   }
   if (int e = use_device(ctx)) return e;
   return check_launch(e->launch(ctx, output, inputs, scalars), symbol);
+}
+
+extern "C" int ipus_gemm_f16_split_noalloc(ipus_context* ctx, void* output, const void* left,
+                                           const void* right, uint32_t batches, uint32_t rows,
+                                           uint32_t columns, uint32_t inner, int transpose_left,
+                                           int transpose_right, uint64_t left_batch_stride,
+                                           uint64_t right_batch_stride, uint32_t splits,
+                                           int gelu) {
+  if (!ctx || !output || !left || !right) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
+  if (batches > 65535 || splits == 0 || splits > 64)
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "batches must be <= 65535 and splits in 1..64");
+  const uint64_t need = (uint64_t)batches * rows * columns * splits * sizeof(float);
+  if (need > IPUS_SPLIT_SCRATCH_BYTES)
+    return fail(IPUS_ERROR_UNSUPPORTED_COUNT,
+                "split-K partials need %llu bytes; the no-allocation scratch holds %llu",
+                (unsigned long long)need, (unsigned long long)IPUS_SPLIT_SCRATCH_BYTES);
+  if (int e = use_device(ctx)) return e;
+  GemmArgs a;
+  a.out = output;
+  a.left = left;
+  a.right = right;
+  a.batches = batches;
+  a.rows = rows;
+  a.columns = columns;
+  a.inner = inner;
+  a.transpose_left = transpose_left != 0;
+  a.transpose_right = transpose_right != 0;
+  a.left_batch_stride = left_batch_stride;
+  a.right_batch_stride = right_batch_stride;
+  a.gelu = gelu != 0;
+  return check_launch(launch_gemm_f16_split_noalloc(ctx->stream, ctx->device, a, splits),
+                      "ipus_gemm_f16_split_noalloc");
 }
 
 // ---------------------------------------------------------------------------
