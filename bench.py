@@ -10,13 +10,27 @@ D128), the memory chain (transpose, block-major 64x64, row reduce on
 X[8192, 8192]), GELU on the MLP hidden [4096, 16384], the MLP graph through
 build_package, and the 256^3 GEMM of configs[0].
 
-Timing: HIP events recorded on the library's stream around K launches after
-W warmups; bandwidth kernels rotate 3 buffer sets (768 MiB > the 256 MiB
-MALL).  One JSON line on stdout.
+Timing: the headline runs W warmups, then exactly K launches with a HIP
+event recorded on the library's stream before each launch and after the
+last, so every launch has its own duration; `value` and `ms_per_step` come
+from the median launch, `roofline.achieved` from the mean (the average
+launch duration that rocprof's kernel statistics report).  The other legs
+time 5 regions of back-to-back launches between two events each (no
+per-launch event gaps for short kernels) and report the median region.
+Bandwidth kernels rotate 3 buffer sets (768 MiB > the 256 MiB MALL).  One
+JSON line on stdout.
+
+Other modes turn rocprofv3 output of a bench run into the committed
+summaries under profiles/ through the package's own rocprof ingestion
+(ipu-stack_amd/profiling.py): --summarize-trace (kernel durations per kernel,
+warmup launches excluded) and --summarize-traffic (HBM bytes per launch from
+FETCH_SIZE / WRITE_SIZE, scaled by the plain copy kernel's counters).
 """
 from __future__ import annotations
 
 import argparse
+import glob
+import hashlib
 import json
 import os
 import sys
@@ -38,19 +52,63 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed(ctx, fn, steps: int, warmup: int) -> float:
-    """Average milliseconds per call of `fn` (which enqueues on the stream)."""
+class Timing(dict):
+    """Per-launch milliseconds of one timed region: median, mean, min, max."""
+
+    @property
+    def median(self) -> float:
+        return self["median_ms"]
+
+    @property
+    def mean(self) -> float:
+        return self["mean_ms"]
+
+
+def timed(ctx, fn, steps: int, warmup: int, per_launch: bool = False,
+          repeats: int = 5) -> Timing:
+    """`warmup` untimed calls of `fn` (which enqueues on the stream) and a
+    synchronisation, then timed calls on HIP events.  per_launch: `steps`
+    calls with an event before each and after the last, so each call has its
+    own duration (the headline: exactly K timed steps).  Otherwise `repeats`
+    regions of `steps` back-to-back calls between two events each, so short
+    kernels carry no per-launch event gaps; the median is over the regions'
+    per-call means."""
     for _ in range(warmup):
         fn(0)
     ctx.sync()
-    timer = ctx.timer()
-    timer.start()
-    for i in range(steps):
-        fn(i)
-    ms = timer.stop()
-    ctx.sync()
-    timer.close()
-    return ms / steps
+    if per_launch:
+        events = ctx.event_series(steps + 1)
+        for i in range(steps):
+            events.record(i)
+            fn(i)
+        events.record(steps)
+        d = np.asarray(events.durations(), dtype=np.float64)
+        ctx.sync()
+        events.close()
+        return Timing(median_ms=float(np.median(d)), mean_ms=float(d.mean()),
+                      min_ms=float(d.min()), max_ms=float(d.max()), launches=int(d.size))
+    regions = []
+    for r in range(repeats):
+        events = ctx.event_series(2)
+        events.record(0)
+        for i in range(steps):
+            fn(r * steps + i)
+        events.record(1)
+        regions.append(events.durations()[0] / steps)
+        ctx.sync()
+        events.close()
+    d = np.asarray(regions, dtype=np.float64)
+    return Timing(median_ms=float(np.median(d)), mean_ms=float(d.mean()), min_ms=float(d.min()),
+                  max_ms=float(d.max()), launches=steps * repeats)
+
+
+def leg_entry(t: Timing, work: float, unit: str, peak: float) -> dict:
+    """A results{} entry: rate from the median launch, its fraction of the
+    spec peak, and the mean launch."""
+    scale = 1e12 if unit == "tflops" else 1e9
+    rate = work / (t.median * 1e-3) / scale
+    return {"ms": round(t.median, 5), "ms_mean": round(t.mean, 5), unit: round(rate, 2),
+            "frac_peak": round(rate / peak, 4)}
 
 
 def gemm_scalars(n, m=None, k=None):
@@ -59,12 +117,12 @@ def gemm_scalars(n, m=None, k=None):
     return [1, m, n, k, 0, 0, 0, 0]
 
 
-def bench_gemm_f16(ipus, ctx, n, steps, warmup):
+def bench_gemm_f16(ipus, ctx, n, steps, warmup, per_launch=False):
     a = ctx.upload(ipus.synth_f16(n * n, 2024, 1, ipus.UNIFORM))
     b = ctx.upload(ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM))
     c = ctx.alloc(n * n * 2)
     ms = timed(ctx, lambda i: ctx.launch("ipu_stack_gemm_f16", c, [a, b], gemm_scalars(n)),
-               steps, warmup)
+               steps, warmup, per_launch=per_launch)
     for x in (a, b, c):
         x.free()
     return ms
@@ -165,45 +223,174 @@ def mfma_calibration(ipus, ctx, blocks=1024, iterations=4096):
         ops = ctx.upload(frags)
         res = ctx.alloc(16 + blocks * 256 * 4)
         sc = [4096, iterations, blocks]
-        ms = timed(ctx, lambda i: ctx.launch("ipus_calibrate_mfma_f16", res, [ops], sc), 3, 1)
+        t = timed(ctx, lambda i: ctx.launch("ipus_calibrate_mfma_f16", res, [ops], sc), 3, 1)
         clocks = res.download(np.uint64)[:2]
         flops = blocks * 4 * 8 * iterations * 32 * 32 * 16 * 2.0
         mhz = clocks[0] / (clocks[1] / 100.0) if clocks[1] else 0.0
-        out[name] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "clock_mhz": round(mhz)}
+        out[name] = {"tflops": round(flops / (t.median * 1e-3) / 1e12, 1),
+                     "clock_mhz": round(mhz)}
         ops.free()
         res.free()
     return out
 
 
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (a C restatement of the reference's
+# diagnostic::evaluate, oracle/) timed on the host's cores, on rank 0 only.
+# ---------------------------------------------------------------------------
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_seconds(fn, min_seconds: float, max_reps: int = 20) -> tuple:
+    times = []
+    while not times or (sum(times) < min_seconds and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times), float(sum(times))
+
+
 def cpu_baseline(ipus, n=8192, min_seconds=10.0):
-    """The repo's CPU evaluator (oracle/, a C restatement of the reference's
-    diagnostic::evaluate GEMM) on the headline workload itself: the full
-    8192^3 fp16 GEMM, repeated until at least `min_seconds` of CPU work; the
-    reported rate is the median over the repetitions."""
+    """The headline workload on the CPU evaluator: the full 8192^3 fp16 GEMM
+    (fp16 -> fp32 operands, blocked AVX2 sgemm, one fp16 rounding) repeated
+    until at least `min_seconds`, median reported; then the other configs on
+    bounded samples (each labelled), and configs[0] single-threaded."""
     from oracle import oracle
     threads = oracle.threads()
     a = ipus.synth_f16(n * n, 2024, 1, ipus.UNIFORM)
     b = ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM)
-    times = []
-    while not times or (sum(times) < min_seconds and len(times) < 20):
-        t0 = time.perf_counter()
-        oracle.gemm_f16(a, b, n, n, n, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    dt = float(np.median(times))
-    return {
+    dt, reps, total = _median_seconds(lambda: oracle.gemm_f16(a, b, n, n, n, nthreads=threads),
+                                      min_seconds)
+    del a, b
+    out = {
         "value": round(2.0 * n ** 3 / dt / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"full 8192^3 fp16 GEMM x{len(times)} (fp16->fp32 operands, blocked AVX2 "
-                  f"sgemm, fp16 rounding), median {dt:.2f} s, total {sum(times):.1f} s",
+        "model": cpu_model(),
+        "sample": f"full 8192^3 fp16 GEMM x{reps} (fp16->fp32 operands, blocked AVX2 sgemm, "
+                  f"fp16 rounding), median {dt:.2f} s, total {total:.1f} s",
     }
+    out["configs"] = cpu_configs(ipus, oracle, threads)
+    return out
+
+
+def cpu_configs(ipus, oracle, threads):
+    """CPU times of the other BASELINE configs on the oracle, each on a
+    bounded sample of the same workload, labelled."""
+    res = {}
+    # configs[0]: 256^3 fp16 GEMM, one thread and all threads.
+    m = 256
+    a = ipus.synth_f16(m * m, 7, 1, ipus.UNIFORM)
+    b = ipus.synth_f16(m * m, 7, 2, ipus.UNIFORM)
+    for label, th in (("single_thread", 1), ("threads", threads)):
+        dt, reps, _ = _median_seconds(lambda: oracle.gemm_f16(a, b, m, m, m, nthreads=th), 1.0, 200)
+        res[f"gemm_f16_256_{label}"] = {"ms": round(dt * 1e3, 3), "threads": th,
+                                        "gflops": round(2.0 * m ** 3 / dt / 1e9, 2),
+                                        "sample": f"full 256^3, median of {reps}"}
+    # configs[2]: fp32 GEMM 4096^3 (full).
+    n = 4096
+    af = ipus.synth_f32(n * n, 4096, 1, ipus.NORMAL)
+    bf = ipus.synth_f32(n * n, 4096, 2, ipus.NORMAL)
+    dt, reps, _ = _median_seconds(lambda: oracle.gemm_f32(af, bf, n, n, n, nthreads=threads), 2.0, 5)
+    res["gemm_f32_4096"] = {"ms": round(dt * 1e3, 1), "tflops": round(2.0 * n ** 3 / dt / 1e12, 4),
+                            "sample": f"full 4096^3, median of {reps}"}
+    del af, bf
+    # configs[3]: MLP 4096 x 4096 . 4096 x 16384 -> GELU -> . 16384 x 4096 (full).
+    x = ipus.synth_f16(4096 * 4096, 9, 1, ipus.NORMAL)
+    w1 = ipus.synth_f16(4096 * 16384, 9, 2, ipus.NORMAL, 0.02)
+    w2 = ipus.synth_f16(16384 * 4096, 9, 3, ipus.NORMAL, 0.02)
+    t0 = time.perf_counter()
+    h = oracle.gelu_f16(oracle.gemm_f16(x, w1, 4096, 16384, 4096, nthreads=threads))
+    oracle.gemm_f16(h, w2, 4096, 4096, 16384, nthreads=threads)
+    dt = time.perf_counter() - t0
+    res["mlp"] = {"ms": round(dt * 1e3, 1), "tflops": round(2 * 2.0 * 4096 * 4096 * 16384 / dt / 1e12, 4),
+                  "sample": "full MLP once (two GEMMs and the GELU)"}
+    del x, w1, w2, h
+    # configs[4]: the memory chain on X[8192, 8192] (full).
+    n = 8192
+    xs = ipus.synth_f16(n * n, 77, 10, ipus.NORMAL)
+    t0 = time.perf_counter()
+    tr = oracle.transpose_u16(xs, 1, n, n)
+    t1 = time.perf_counter()
+    bm = oracle.rearrange_row_major_f16(tr, ipus.ORDER_BLOCK_MAJOR, 1, n, n, n, n, 64, 64)
+    t2 = time.perf_counter()
+    oracle.reduce_rows_block_major_f16(bm, 64, 64, n, n, nthreads=threads)
+    t3 = time.perf_counter()
+    for key, sec, nbytes in (("transpose", t1 - t0, 4 * n * n), ("block_major", t2 - t1, 4 * n * n),
+                             ("reduce_rows", t3 - t2, 2 * n * n + 4 * n)):
+        res[key] = {"ms": round(sec * 1e3, 1), "gbps": round(nbytes / sec / 1e9, 2),
+                    "sample": "full 8192^2 once"}
+    del xs, tr, bm
+    # configs[5]: attention B8 H16 D128 on evenly spaced query rows of every
+    # stream, extrapolated to all rows (labelled as such).
+    streams, d = 128, 128
+    for causal, s in ((True, 4096), (False, 2048)):
+        nq = streams * s * d
+        q = oracle.f16_to_f32(ipus.synth_f16(nq, 5, 1, ipus.NORMAL))
+        k = oracle.f16_to_f32(ipus.synth_f16(nq, 5, 2, ipus.NORMAL))
+        v = oracle.f16_to_f32(ipus.synth_f16(nq, 5, 3, ipus.NORMAL))
+        per_stream = 8
+        rows = np.array([st * s + r for st in range(streams)
+                         for r in np.linspace(0, s - 1, per_stream).astype(np.int64)], np.uint32)
+        t0 = time.perf_counter()
+        oracle.attention(q, k, v, streams, s, s, d, d, causal, row_list=rows, nthreads=threads)
+        dt = (time.perf_counter() - t0) * (streams * s) / rows.size
+        fl = 4.0 * streams * d * (s * (s + 1) / 2 if causal else s * s)
+        key = f"attention_{'causal' if causal else 'noncausal'}_s{s}"
+        res[key] = {"ms": round(dt * 1e3, 1), "tflops": round(fl / dt / 1e12, 5),
+                    "sample": f"{rows.size} evenly spaced query rows ({per_stream} per stream), "
+                              f"time extrapolated x{streams * s // rows.size} to every row"}
+        del q, k, v
+    return res
+
+
+# ---------------------------------------------------------------------------
+# roofline.traffic: HBM bytes per launch from the committed rocprofv3 --pmc
+# summary, used only when it was measured on the current kernel sources.
+# ---------------------------------------------------------------------------
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "gemm_f16_8192_traffic.json")
+GEMM_SOURCES = ("ipu-stack_amd/csrc/k_gemm_f16.hip", "ipu-stack_amd/csrc/device_common.h")
+
+
+def source_digest(paths=GEMM_SOURCES) -> str:
+    h = hashlib.sha256()
+    for rel in paths:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def committed_traffic():
+    """(bytes per launch, note): the traffic summary's figure if its kernel
+    source digest equals the current sources', else (None, why)."""
+    if not os.path.exists(TRAFFIC_JSON):
+        return None, "no traffic summary"
+    with open(TRAFFIC_JSON) as f:
+        t = json.load(f)
+    digest = source_digest()
+    if t.get("kernel_source_digest") != digest:
+        return None, (f"traffic summary measured on kernel sources {t.get('kernel_source_digest')}, "
+                      f"current {digest}")
+    return t.get("hbm_bytes_per_launch"), (
+        f"profiles/gemm_f16_8192_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
+        f"the same kernel sources ({digest}), scaled by the copy kernel's counters")
 
 
 def traffic_probe(ipus, ctx, n=8192, copy_bytes=256 << 20):
     """Untimed launches for the rocprofv3 --pmc passes that give
     roofline.traffic: the headline GEMM, then a plain 16-byte-vector copy of
-    `copy_bytes` whose FETCH_SIZE / WRITE_SIZE calibrate the counters' unit."""
+    `copy_bytes` with ordinary loads and stores whose FETCH_SIZE / WRITE_SIZE
+    calibrate the counters' unit (and the library's streaming copy, whose
+    non-temporal accesses the counters weigh differently, for comparison)."""
     a = ctx.upload(ipus.synth_f16(n * n, 2024, 1, ipus.UNIFORM))
     b = ctx.upload(ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM))
     c = ctx.alloc(n * n * 2)
@@ -212,22 +399,113 @@ def traffic_probe(ipus, ctx, n=8192, copy_bytes=256 << 20):
     ctx.sync()
     src, dst = ctx.alloc(copy_bytes), ctx.alloc(copy_bytes)
     ctx.memset(src, 1)
-    for _ in range(3):
-        ctx.launch("ipu_stack_copy", dst, [src], [copy_bytes])
+    for symbol in ("ipus_calibrate_copy", "ipu_stack_copy"):
+        for _ in range(3):
+            ctx.launch(symbol, dst, [src], [copy_bytes])
     ctx.sync()
     for x in (a, b, c, src, dst):
         x.free()
-    log(f"traffic probe: 3x gemm_f16 {n}^3, 3x copy {copy_bytes} B")
+    log(f"traffic probe: 3x gemm_f16 {n}^3, 3x plain copy and 3x streaming copy of "
+        f"{copy_bytes} B")
 
 
-def committed_traffic():
-    """HBM bytes per launch of the headline kernel from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE runs (profiles/gemm_f16_8192_traffic.json)."""
-    path = os.path.join(ROOT, "profiles", "gemm_f16_8192_traffic.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+# ---------------------------------------------------------------------------
+# Summaries of rocprofv3 output through the package's ProfileReport ingestion
+# ---------------------------------------------------------------------------
+def _profiling():
+    __graft_entry__.import_package()
+    import ipu_stack_amd.profiling as prof
+    return prof
+
+
+def _timed_phases(report, skip_per_kernel: int) -> frozenset:
+    """Dispatch phases left after dropping each kernel's first
+    `skip_per_kernel` dispatches (the warmups)."""
+    seen = {}
+    keep = set()
+    for tile in report.tiles:
+        for sample in sorted(tile.samples, key=lambda x: x.step.phase):
+            k = sample.step.kernel
+            seen[k] = seen.get(k, 0) + 1
+            if seen[k] > skip_per_kernel:
+                keep.add(sample.step.phase)
+    return frozenset(keep)
+
+
+def summarize_trace(directory: str, skip: int, command: str) -> str:
+    prof = _profiling()
+    report = prof.from_rocprof(directory)
+    keep = _timed_phases(report, skip)
+    q = prof.query(report, prof.Query(group_by=prof.GroupBy.KERNEL, phases=keep, shared_clock=True))
+    lines = [f"Command (from the repository root, `export TMPDIR=/tmp`):", "",
+             f"    {command}", "",
+             f"Summary: `python bench.py --summarize-trace <trace dir> --skip {skip}` "
+             f"(ipu-stack_amd/profiling.py: rocprofv3 kernel trace -> ProfileReport -> query "
+             f"grouped by kernel); each kernel's first {skip} dispatches (warmups) are excluded.",
+             "", "| kernel | dispatches | mean ns | p50 ns | p95 ns | max ns |",
+             "|---|---|---|---|---|---|"]
+    for g in q.groups:
+        lines.append(f"| `{g.name}` | {g.sample_count} | {g.mean_cycles:.0f} | {g.p50_cycles} | "
+                     f"{g.p95_cycles} | {g.maximum_cycles} |")
+    return "\n".join(lines) + "\n"
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str, kernel: str, copy_kernel: str,
+                      copy_bytes: int, algorithmic: float, skip: int, commands: list) -> dict:
+    """HBM bytes per launch of `kernel` from FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by the factor that makes the copy kernel's counter
+    equal its known bytes."""
+    prof = _profiling()
+
+    def per_kernel(directory, counter):
+        report = prof.from_rocprof(counter_csv=directory)
+        keep = _timed_phases(report, skip)
+        vals = {}
+        for tile in report.tiles:
+            for smp in tile.samples:
+                if smp.step.phase not in keep:
+                    continue
+                md = {m.name: m.value for m in smp.step.metadata}
+                v = md.get(prof.COUNTER_PREFIX + counter)
+                if v is not None:
+                    vals.setdefault(smp.step.kernel, []).append(float(v) * 1024.0)
+        return {k: float(np.mean(v)) for k, v in vals.items()}
+
+    fetch = per_kernel(fetch_dir, "FETCH_SIZE")
+    write = per_kernel(write_dir, "WRITE_SIZE")
+    pick = lambda table, name: next(v for k, v in table.items() if k.startswith(name))  # noqa: E731
+    f_scale = copy_bytes / pick(fetch, copy_kernel)
+    w_scale = copy_bytes / pick(write, copy_kernel)
+    fb, wb = pick(fetch, kernel) * f_scale, pick(write, kernel) * w_scale
+    return {
+        "kernel": kernel, "kernel_source_digest": source_digest(),
+        "fetch_bytes_per_launch": round(fb), "write_bytes_per_launch": round(wb),
+        "hbm_bytes_per_launch": round(fb + wb),
+        "algorithmic_bytes_per_launch": algorithmic,
+        "traffic_over_algorithmic": round((fb + wb) / algorithmic, 3),
+        "counter_scale": {"FETCH_SIZE": round(f_scale, 4), "WRITE_SIZE": round(w_scale, 4),
+                          "calibration": f"{copy_kernel} of {copy_bytes} bytes read and written"},
+        "raw_bytes_per_dispatch": {"FETCH_SIZE": {k: round(v) for k, v in fetch.items()},
+                                   "WRITE_SIZE": {k: round(v) for k, v in write.items()}},
+        "commands": commands,
+        "summary": "python bench.py --summarize-traffic <FETCH_SIZE dir> <WRITE_SIZE dir>",
+    }
+
+
+def device_name(info: dict) -> str:
+    """The HIP device name; where the runtime leaves it empty, the product
+    name the amdgpu driver exposes in sysfs."""
+    if info.get("name"):
+        return info["name"]
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/product_name")):
+        try:
+            with open(path) as f:
+                text = f.read().strip()
+            if text:
+                return text
+        except OSError:
+            continue
+    return f"AMD GPU {info.get('arch', '').split(':')[0]} ({info.get('compute_units')} CUs)"
 
 
 LEGS = ("mfma_calibration", "gemm_f32_4096", "gemm_f16_256", "attention_causal_s4096",
@@ -250,46 +528,36 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
         results["mfma_calibration"] = cal
         log(f"mfma calibration: {cal}")
     if want("gemm_f32_4096"):
-        ms32 = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2)
-        t32 = 2.0 * 4096 ** 3 / (ms32 * 1e-3) / 1e12
-        results["gemm_f32_4096"] = {"ms": round(ms32, 5), "tflops": round(t32, 2),
-                                    "frac_peak": round(t32 / PEAK_FP32_TFLOPS, 4)}
-        log(f"gemm_f32 4096^3: {ms32:.4f} ms {t32:.1f} TFLOP/s")
+        t = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2)
+        results["gemm_f32_4096"] = leg_entry(t, 2.0 * 4096 ** 3, "tflops", PEAK_FP32_TFLOPS)
+        log(f"gemm_f32 4096^3: {results['gemm_f32_4096']}")
     if want("gemm_f16_256"):
-        ms256 = bench_gemm_f16(ipus, ctx, 256, 50, 5)
-        results["gemm_f16_256"] = {"ms": round(ms256, 5),
-                                   "tflops": round(2.0 * 256 ** 3 / (ms256 * 1e-3) / 1e12, 3)}
+        t = bench_gemm_f16(ipus, ctx, 256, 50, 5)
+        results["gemm_f16_256"] = leg_entry(t, 2.0 * 256 ** 3, "tflops", PEAK_FP16_TFLOPS)
     for causal, s in ((True, 4096), (False, 2048)):
         key = f"attention_{'causal' if causal else 'noncausal'}_s{s}"
         if not want(key):
             continue
-        msa = bench_attention(ipus, ctx, s, causal, sub_steps, 2)
+        t = bench_attention(ipus, ctx, s, causal, sub_steps, 2)
         fl = 4.0 * 128 * 128 * (s * (s + 1) / 2 if causal else s * s)
-        ta = fl / (msa * 1e-3) / 1e12
-        results[key] = {"ms": round(msa, 5), "tflops": round(ta, 2),
-                        "frac_peak": round(ta / PEAK_FP16_TFLOPS, 4)}
-        log(f"{key}: {msa:.4f} ms {ta:.1f} TFLOP/s")
+        results[key] = leg_entry(t, fl, "tflops", PEAK_FP16_TFLOPS)
+        log(f"{key}: {results[key]}")
     if want("memory_chain"):
         chain = bench_memory_chain(ipus, ctx, args.steps, 3)
         bytes_rw = {"copy": 2 * n * n * 2, "transpose": 2 * n * n * 2, "block_major": 2 * n * n * 2,
                     "reduce_rows": n * n * 2 + n * 4, "reduce_rows_row_major": n * n * 2 + n * 4}
-        for k, v in chain.items():
-            gbps = bytes_rw[k] / (v * 1e-3) / 1e9
-            results[k] = {"ms": round(v, 5), "gbps": round(gbps, 1),
-                          "frac_peak": round(gbps / PEAK_HBM_GBPS, 4)}
-            log(f"{k}: {v * 1e3:.1f} us {gbps:.0f} GB/s")
+        for k, t in chain.items():
+            results[k] = leg_entry(t, bytes_rw[k], "gbps", PEAK_HBM_GBPS)
+            log(f"{k}: {results[k]}")
     if want("gelu_4096x16384"):
-        msg = bench_gelu(ipus, ctx, args.steps, 3)
-        gg = 2 * 4096 * 16384 * 2 / (msg * 1e-3) / 1e9
-        results["gelu_4096x16384"] = {"ms": round(msg, 5), "gbps": round(gg, 1),
-                                      "frac_peak": round(gg / PEAK_HBM_GBPS, 4)}
-        log(f"gelu: {msg * 1e3:.1f} us {gg:.0f} GB/s")
+        t = bench_gelu(ipus, ctx, args.steps, 3)
+        results["gelu_4096x16384"] = leg_entry(t, 2 * 4096 * 16384 * 2, "gbps", PEAK_HBM_GBPS)
+        log(f"gelu: {results['gelu_4096x16384']}")
     if want("mlp_graph"):
-        msm = bench_mlp_graph(ipus, ctx, 5, 1)
-        tm = 2 * 2.0 * 4096 * 4096 * 16384 / (msm * 1e-3) / 1e12
-        results["mlp_graph"] = {"ms": round(msm, 5), "tflops": round(tm, 2),
-                                "frac_peak": round(tm / PEAK_FP16_TFLOPS, 4)}
-        log(f"mlp graph: {msm:.3f} ms {tm:.1f} TFLOP/s")
+        t = bench_mlp_graph(ipus, ctx, args.steps, 3)
+        results["mlp_graph"] = leg_entry(t, 2 * 2.0 * 4096 * 4096 * 16384, "tflops",
+                                         PEAK_FP16_TFLOPS)
+        log(f"mlp graph: {results['mlp_graph']}")
     return results
 
 
@@ -304,7 +572,24 @@ def main() -> int:
                     help="only launch the headline GEMM and a calibration copy (for --pmc)")
     ap.add_argument("--leg", action="append", choices=LEGS,
                     help="run only these secondary legs (no headline; for profiling)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="markdown summary of a rocprofv3 --kernel-trace output directory")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="JSON traffic summary of two rocprofv3 --pmc runs of --traffic-probe")
+    ap.add_argument("--skip", type=int, default=5, help="warmup dispatches per kernel to drop")
+    ap.add_argument("--command", default="", help="command line recorded in a summary")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.skip, args.command), end="")
+        return 0
+    if args.summarize_traffic:
+        n = 8192
+        out = summarize_traffic(args.summarize_traffic[0], args.summarize_traffic[1],
+                                "gemm_f16_256_kernel", "copy_plain_kernel", 256 << 20,
+                                3.0 * n * n * 2, args.skip,
+                                [c for c in args.command.split(" ;; ") if c])
+        print(json.dumps(out, indent=1))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested); run with --gpus 1.", file=sys.stderr)
@@ -315,7 +600,8 @@ def main() -> int:
     ipus.load_library()
     ctx = ipus.Context(0)
     info = ctx.device_info()
-    log(f"device: {info['name']} {info['arch']} CUs={info['compute_units']} "
+    name = device_name(info)
+    log(f"device: {name} {info['arch']} CUs={info['compute_units']} "
         f"clock={info['clock_khz'] / 1e3:.0f} MHz")
 
     if args.traffic_probe:
@@ -331,15 +617,17 @@ def main() -> int:
     n = 8192
     flops = 2.0 * n ** 3
     log("headline: gemm_f16 8192^3")
-    ms = bench_gemm_f16(ipus, ctx, n, args.steps, args.warmup)
-    tflops = flops / (ms * 1e-3) / 1e12
-    log(f"  {ms:.4f} ms/step  {tflops:.1f} TFLOP/s")
+    t = bench_gemm_f16(ipus, ctx, n, args.steps, args.warmup, per_launch=True)
+    tflops = flops / (t.median * 1e-3) / 1e12
+    achieved = flops / (t.mean * 1e-3) / 1e12
+    log(f"  median {t.median:.4f} ms/step ({tflops:.1f} TFLOP/s), mean {t.mean:.4f} ms")
 
-    results = {"gemm_f16_8192": {"ms": round(ms, 5), "tflops": round(tflops, 2),
-                                 "frac_peak": round(tflops / PEAK_FP16_TFLOPS, 4)}}
+    results = {"gemm_f16_8192": dict(leg_entry(t, flops, "tflops", PEAK_FP16_TFLOPS),
+                                     min_ms=round(t["min_ms"], 5), max_ms=round(t["max_ms"], 5))}
     if not args.only_headline:
         results.update(secondary_legs(ipus, ctx, args, tflops))
 
+    traffic, traffic_note = committed_traffic()
     line = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -347,7 +635,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(t.median, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -355,12 +643,16 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "gemm_f16 M=N=K=8192, A,B ~ U[-1,1] fp16, fp32 accumulate, "
                                "fp16 out (BASELINE configs[1])",
-                   "M": n, "N": n, "K": n, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-                     "traffic": committed_traffic()},
+                   "M": n, "N": n, "K": n, "parallelism": "single GPU",
+                   "statistic": "value and ms_per_step: median launch of the K timed launches; "
+                                "roofline.achieved: their mean (rocprof's average)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                     "traffic": traffic, "traffic_source": traffic_note,
+                     "kernel": "gemm_f16_256_kernel<false, false, false, false, false>",
+                     "ms_mean": round(t.mean, 5)},
         "results": results,
-        "device": {"name": info["name"], "arch": info["arch"], "cus": info["compute_units"]},
+        "device": {"name": name, "arch": info["arch"], "cus": info["compute_units"]},
     }
     ctx.close()
     if rank == 0 and not args.no_cpu_baseline:

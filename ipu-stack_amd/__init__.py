@@ -482,6 +482,9 @@ class Context:
     def timer(self) -> "Timer":
         return Timer(self)
 
+    def event_series(self, count: int) -> "EventSeries":
+        return EventSeries(self, count)
+
 
 class Timer:
     """HIP events recorded on the context stream."""
@@ -506,6 +509,37 @@ class Timer:
     def close(self) -> None:
         _lib().ipus_event_destroy(self.start_event)
         _lib().ipus_event_destroy(self.end_event)
+
+
+class EventSeries:
+    """`count` HIP events recorded on the context stream between launches:
+    event i before launch i and event count - 1 after the last one, so
+    durations()[i] is launch i's time on the stream (back-to-back launches)."""
+
+    def __init__(self, context: Context, count: int):
+        self.context = context
+        self.events = []
+        for _ in range(count):
+            e = ctypes.c_void_p()
+            _check(_lib().ipus_event_create(context.handle, ctypes.byref(e)))
+            self.events.append(e.value)
+
+    def record(self, i: int) -> None:
+        _check(_lib().ipus_event_record(self.context.handle, self.events[i]))
+
+    def durations(self) -> list:
+        """Milliseconds between consecutive events (waits for the last)."""
+        out = []
+        ms = ctypes.c_float(0)
+        for a, b in zip(self.events, self.events[1:]):
+            _check(_lib().ipus_event_elapsed_ms(a, b, ctypes.byref(ms)))
+            out.append(ms.value)
+        return out
+
+    def close(self) -> None:
+        for e in self.events:
+            _lib().ipus_event_destroy(e)
+        self.events = []
 
 
 # ---------------------------------------------------------------------------

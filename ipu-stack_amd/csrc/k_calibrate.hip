@@ -48,7 +48,30 @@ __global__ __launch_bounds__(256) void mfma_calibrate_kernel(uint64_t* __restric
   }
 }
 
+// Plain copy for the HBM traffic counters' calibration: ordinary (temporal)
+// 16-byte loads and stores, one vector per thread, so its FETCH_SIZE /
+// WRITE_SIZE read as a kernel whose loads take the ordinary cache path (the
+// library's streaming copy uses non-temporal accesses, which the counters
+// weigh differently).
+__global__ __launch_bounds__(256) void copy_plain_kernel(u32x4* __restrict__ dst,
+                                                         const u32x4* __restrict__ src,
+                                                         uint64_t vectors) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < vectors) dst[i] = src[i];
+}
+
 }  // namespace
+
+int launch_calibrate_copy(hipStream_t stream, void* dst, const void* src, uint32_t bytes) {
+  if (bytes % 16 != 0 || (uintptr_t)dst % 16 != 0 || (uintptr_t)src % 16 != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  const uint64_t vectors = bytes / 16;
+  if (vectors == 0) return 0;
+  hipLaunchKernelGGL(copy_plain_kernel, dim3((uint32_t)((vectors + 255) / 256)), dim3(256), 0,
+                     stream, (u32x4*)dst, (const u32x4*)src, vectors);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e;
+}
 
 uint64_t calibrate_output_bytes(uint32_t blocks) { return 16 + (uint64_t)blocks * 256 * 4; }
 

@@ -101,6 +101,9 @@ int launch_split_heads(hipStream_t stream, void* dst, const void* src, uint32_t 
 // clock cycles, 100 MHz ticks of lane 0 of block 0) and a float sink of
 // blocks * 256 values; `operands` holds operand_count fragments of 8 fp16.
 uint64_t calibrate_output_bytes(uint32_t blocks);
+// Plain 16-byte-vector copy with ordinary loads and stores (bytes % 16 == 0,
+// both pointers 16-byte aligned): the HBM traffic counters' calibration.
+int launch_calibrate_copy(hipStream_t stream, void* dst, const void* src, uint32_t bytes);
 int launch_calibrate_mfma_f16(hipStream_t stream, void* out, const void* operands,
                               uint32_t operand_count, uint32_t iterations, uint32_t blocks);
 // Stored order (AmpLeft, AmpTransposedRight, BlockMajor) -> row-major.
