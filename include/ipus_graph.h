@@ -51,11 +51,17 @@ typedef uint32_t ipus_sequence; /* ValueSequenceId */
 #define IPUS_PRECISION_F16 1
 #define IPUS_PRECISION_F32 2
 
-/* Physical orders of a stored tensor (layout.rs:7-30 plus row-major). */
+/* Physical orders of a stored tensor (ElementOrder, layout.rs:5-45).  The
+ * first four are also the orders ipus_graph_rearrange produces; the others
+ * occur only as declared input formats. */
 #define IPUS_ORDER_AMP_LEFT 0
 #define IPUS_ORDER_AMP_TRANSPOSED_RIGHT 1
 #define IPUS_ORDER_BLOCK_MAJOR 2
 #define IPUS_ORDER_ROW_MAJOR 3
+#define IPUS_ORDER_AMP_OUTPUT 4
+#define IPUS_ORDER_AMP_TRANSPOSED_LEFT 5
+#define IPUS_ORDER_AMP_TRANSPOSED_OUTPUT 6
+#define IPUS_ORDER_BLOCK_MAJOR_TRANSPOSED 7
 
 int ipus_graph_create(ipus_graph **out);
 int ipus_graph_destroy(ipus_graph *graph);
@@ -102,9 +108,61 @@ int ipus_graph_value_shape(const ipus_graph *graph, ipus_value value, uint32_t *
 int ipus_graph_operation_count(const ipus_graph *graph, int *count);
 
 /* ---- package ---- */
+
+/* One tiled axis of a tensor layout: AxisTiling (layout.rs:140-175).
+ * `axis` counts from the start (from_end = 0) or, from 1, from the end
+ * (from_end = 1), as TensorAxis::FromStart / FromEnd (layout.rs:115-131).
+ * Zero-valued padding_groups, padding_multiple and shard_padding_multiple
+ * take AxisTiling::new's defaults (1, block_size, 1); tile_stride 0 packs the
+ * axis after the replicas and the preceding axes (axis_strides,
+ * layout.rs:234-251). */
+typedef struct ipus_axis_tiling {
+  int from_end;
+  uint32_t axis;
+  uint32_t partitions;
+  uint32_t padding_groups;
+  uint32_t block_size;
+  uint32_t padding_multiple;
+  uint32_t shard_padding_multiple;
+  int zero_padding; /* Padding::Zero (1) or Padding::Reject (0) */
+  uint32_t tile_stride;
+} ipus_axis_tiling;
+
+#define IPUS_MAX_TILED_AXES 4
+
+/* TensorFormat{precision, layout} (layout.rs:808-811) of a host-bound
+ * tensor: the element order inside every shard (row_block / column_block for
+ * the block-major orders) and the TensorTiling (layout.rs:205-210) that cuts
+ * the tensor into tile_count shards.  The host bytes of such a tensor are
+ * the shards' storage in logical tile order, each padded per its tiling, as
+ * CompiledTensor::binding lays out the reference's binding file
+ * (package.rs:2101-2137).  axis_count = 0 with tile_count = replicas = 1 is
+ * one unsharded tensor in `order`.  AMP and block-major orders need F16. */
+typedef struct ipus_tensor_format {
+  int precision;
+  int order;
+  uint32_t row_block, column_block;
+  uint32_t tile_count, replicas;
+  int axis_count;
+  ipus_axis_tiling axes[IPUS_MAX_TILED_AXES];
+} ipus_tensor_format;
+
+/* One entry of PipelineConfig's inputs (config.rs:310-320): with_input
+ * (automatic = 0: the host writes `format`'s bytes and build_package plans
+ * their conversion) or with_automatic_input (automatic = 1: only the
+ * precision is fixed; the input is row-major). */
+typedef struct ipus_input_format {
+  ipus_value value;
+  int automatic;
+  ipus_tensor_format format;
+} ipus_input_format;
+
 typedef struct ipus_package_config {
   int compute_precision;    /* IPUS_PRECISION_F16 (default) or _F32 */
   int attention_output_f16; /* 0: F32 attention output (reference), 1: F16 */
+  int input_format_count;   /* entries in input_formats (inputs not named are
+                               row-major at the compute precision) */
+  const ipus_input_format *input_formats;
 } ipus_package_config;
 
 typedef struct ipus_package ipus_package;
@@ -117,7 +175,8 @@ typedef struct ipus_tensor_info {
   int precision;
   int order;
   uint32_t row_block, column_block;
-  uint64_t bytes;
+  uint64_t bytes;      /* bytes the host writes or reads (all shards) */
+  uint32_t shards;     /* tiles of a declared tiled format, else 1 */
 } ipus_tensor_info;
 
 int ipus_build_package(const ipus_graph *graph, const ipus_package_config *config,

@@ -18,7 +18,7 @@ import ctypes
 import weakref
 import os
 import struct
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from typing import Callable, Iterable, Sequence
 
 import numpy as np
@@ -32,6 +32,11 @@ ORDER_AMP_LEFT = 0
 ORDER_AMP_TRANSPOSED_RIGHT = 1
 ORDER_BLOCK_MAJOR = 2
 ORDER_ROW_MAJOR = 3
+ORDER_AMP_OUTPUT = 4
+ORDER_AMP_TRANSPOSED_LEFT = 5
+ORDER_AMP_TRANSPOSED_OUTPUT = 6
+ORDER_BLOCK_MAJOR_TRANSPOSED = 7
+MAX_TILED_AXES = 4
 
 OK = 0
 ERROR_INVALID_ARGUMENT = -1
@@ -104,11 +109,34 @@ class _TensorInfo(ctypes.Structure):
         ("row_block", ctypes.c_uint32),
         ("column_block", ctypes.c_uint32),
         ("bytes", ctypes.c_uint64),
+        ("shards", ctypes.c_uint32),
     ]
 
 
+class _AxisTiling(ctypes.Structure):
+    _fields_ = [("from_end", ctypes.c_int), ("axis", ctypes.c_uint32),
+                ("partitions", ctypes.c_uint32), ("padding_groups", ctypes.c_uint32),
+                ("block_size", ctypes.c_uint32), ("padding_multiple", ctypes.c_uint32),
+                ("shard_padding_multiple", ctypes.c_uint32), ("zero_padding", ctypes.c_int),
+                ("tile_stride", ctypes.c_uint32)]
+
+
+class _TensorFormat(ctypes.Structure):
+    _fields_ = [("precision", ctypes.c_int), ("order", ctypes.c_int),
+                ("row_block", ctypes.c_uint32), ("column_block", ctypes.c_uint32),
+                ("tile_count", ctypes.c_uint32), ("replicas", ctypes.c_uint32),
+                ("axis_count", ctypes.c_int), ("axes", _AxisTiling * 4)]
+
+
+class _InputFormat(ctypes.Structure):
+    _fields_ = [("value", ctypes.c_uint32), ("automatic", ctypes.c_int),
+                ("format", _TensorFormat)]
+
+
 class _PackageConfig(ctypes.Structure):
-    _fields_ = [("compute_precision", ctypes.c_int), ("attention_output_f16", ctypes.c_int)]
+    _fields_ = [("compute_precision", ctypes.c_int), ("attention_output_f16", ctypes.c_int),
+                ("input_format_count", ctypes.c_int),
+                ("input_formats", ctypes.POINTER(_InputFormat))]
 
 
 _LIB: ctypes.CDLL | None = None
@@ -679,9 +707,182 @@ class ComputeGraph:
 @dataclass
 class PackageConfig:
     """GPU stand-in for PackageConfig (package.rs:89-94): compute precision
-    of GEMM / Add and the attention output precision."""
+    of GEMM / Add and the attention output precision, plus PipelineConfig's
+    per-input formats (config.rs:310-320): `with_input(value, format)` makes
+    the host write that input in the given TensorFormat (shards in tile
+    order, as the reference's binding file), `with_automatic_input(value,
+    precision)` fixes only its precision."""
     compute_precision: str = "f16"
     attention_output_f16: bool = False
+    inputs: dict = field(default_factory=dict)            # value -> TensorFormat
+    automatic_inputs: dict = field(default_factory=dict)  # value -> precision
+
+    def with_input(self, value: int, fmt: "TensorFormat") -> "PackageConfig":
+        self.inputs[value] = fmt
+        self.automatic_inputs.pop(value, None)
+        return self
+
+    def with_automatic_input(self, value: int, precision: int) -> "PackageConfig":
+        self.automatic_inputs[value] = precision
+        self.inputs.pop(value, None)
+        return self
+
+
+# ---------------------------------------------------------------------------
+# Tensor formats of host-bound inputs (crates/ipu-codegen/src/layout.rs)
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class TensorAxis:
+    """TensorAxis::FromStart(i) / FromEnd(i) (layout.rs:115-131)."""
+    index: int
+    from_end: bool = True
+
+    @staticmethod
+    def from_start(i: int) -> "TensorAxis":
+        return TensorAxis(i, False)
+
+    @staticmethod
+    def from_end_(i: int) -> "TensorAxis":
+        return TensorAxis(i, True)
+
+
+PADDING_REJECT, PADDING_ZERO = 0, 1
+
+
+@dataclass(frozen=True)
+class AxisTiling:
+    """AxisTiling (layout.rs:140-197): AxisTiling(axis, partitions,
+    block_size, padding) with the builder methods' fields."""
+    axis: TensorAxis
+    partitions: int
+    block_size: int
+    padding: int = PADDING_REJECT
+    padding_groups: int = 1
+    padding_multiple: int = 0            # 0: block_size (AxisTiling::new)
+    shard_padding_multiple: int = 1
+    tile_stride: int = 0                 # 0: packed after replicas and preceding axes
+
+    def with_tile_stride(self, stride: int) -> "AxisTiling":
+        return replace(self, tile_stride=stride)
+
+    def with_padding_multiple(self, m: int) -> "AxisTiling":
+        return replace(self, padding_multiple=m)
+
+    def with_shard_padding_multiple(self, m: int) -> "AxisTiling":
+        return replace(self, shard_padding_multiple=m)
+
+    def with_padding_groups(self, g: int) -> "AxisTiling":
+        return replace(self, padding_groups=g)
+
+
+@dataclass(frozen=True)
+class Layout:
+    """Layout{order, tiling} (layout.rs:268-275) with the constructors the
+    reference uses for host-bound inputs.  `order` is an ORDER_* code;
+    row_block / column_block belong to the block-major orders."""
+    order: int
+    tile_count: int = 1
+    replicas: int = 1
+    axes: tuple = ()
+    row_block: int = 0
+    column_block: int = 0
+
+    @staticmethod
+    def row_major(tile_count: int = 1, axes=(), replicas: int = 1) -> "Layout":
+        return Layout(ORDER_ROW_MAJOR, tile_count, replicas, tuple(axes))
+
+    @staticmethod
+    def row_sharded(tile_count: int) -> "Layout":            # layout.rs:297-299
+        return Layout.row_major(tile_count, [AxisTiling(TensorAxis(2), tile_count, 1)])
+
+    @staticmethod
+    def head_sharded(tile_count: int) -> "Layout":           # layout.rs:301-303
+        return Layout.row_major(tile_count, [AxisTiling(TensorAxis(3), tile_count, 1)])
+
+    @staticmethod
+    def _attention_tiling(heads: int, query_partitions: int) -> tuple:  # layout.rs:305-316
+        return (AxisTiling(TensorAxis(2), query_partitions, 1).with_tile_stride(heads),
+                AxisTiling(TensorAxis(3), heads, 1).with_tile_stride(1))
+
+    @staticmethod
+    def attention_query(heads: int, query_partitions: int) -> "Layout":  # layout.rs:318-332
+        axes = Layout._attention_tiling(heads, query_partitions) + (
+            AxisTiling(TensorAxis(1), 1, 16, PADDING_ZERO),)
+        return Layout(ORDER_AMP_LEFT, heads * query_partitions, 1, axes)
+
+    @staticmethod
+    def attention_key(heads: int, key_partitions: int) -> "Layout":      # layout.rs:334-356
+        axes = (AxisTiling(TensorAxis(3), heads, 1).with_tile_stride(1),
+                AxisTiling(TensorAxis(2), key_partitions, 64, PADDING_ZERO).with_tile_stride(heads),
+                AxisTiling(TensorAxis(1), 1, 16, PADDING_ZERO))
+        return Layout(ORDER_AMP_TRANSPOSED_RIGHT, heads * key_partitions, 1, axes)
+
+    @staticmethod
+    def attention_block_major_key_value(heads: int, key_partitions: int) -> "Layout":
+        return replace(Layout.attention_key(heads, key_partitions), order=ORDER_BLOCK_MAJOR,
+                       row_block=64, column_block=16)                   # layout.rs:358-365
+
+    @staticmethod
+    def attention_output(heads: int, query_partitions: int) -> "Layout":  # layout.rs:367-375
+        axes = Layout._attention_tiling(heads, query_partitions) + (
+            AxisTiling(TensorAxis(1), 1, 16, PADDING_ZERO),)
+        return Layout(ORDER_ROW_MAJOR, heads * query_partitions, 1, axes)
+
+    @staticmethod
+    def amp_left(inner: int, tile_count: int) -> "Layout":              # layout.rs:376-389
+        return Layout(ORDER_AMP_LEFT, tile_count, 1,
+                      (AxisTiling(TensorAxis(2), tile_count, 1),
+                       AxisTiling(TensorAxis(1), 1, inner, PADDING_ZERO)))
+
+    @staticmethod
+    def amp_output(tile_count: int) -> "Layout":                        # layout.rs:402-418
+        return Layout(ORDER_AMP_OUTPUT, tile_count, 1,
+                      (AxisTiling(TensorAxis(2), tile_count, 1),
+                       AxisTiling(TensorAxis(1), 1, 64, PADDING_ZERO)))
+
+    @staticmethod
+    def block_major_matrix(row_block: int, tile_count: int) -> "Layout":  # layout.rs:391-400
+        return Layout.block_major_matrix_storage(row_block, 64, tile_count, 1, 1)
+
+    @staticmethod
+    def block_major_matrix_storage(inner_block: int, output_column_block: int,
+                                   column_partitions: int, inner_partitions: int,
+                                   copies: int) -> "Layout":              # layout.rs:552-590
+        axes = (AxisTiling(TensorAxis(1), column_partitions, output_column_block,
+                           PADDING_ZERO).with_tile_stride(1),
+                AxisTiling(TensorAxis(2), inner_partitions, inner_block, PADDING_ZERO))
+        return Layout(ORDER_BLOCK_MAJOR, column_partitions * inner_partitions * copies, copies,
+                      axes, inner_block, 16)
+
+    @staticmethod
+    def transposed_block_major_matrix_storage(inner_block: int, output_column_block: int,
+                                              column_partitions: int, inner_partitions: int,
+                                              copies: int) -> "Layout":   # layout.rs:592-630
+        axes = (AxisTiling(TensorAxis(2), column_partitions, output_column_block,
+                           PADDING_ZERO).with_tile_stride(1),
+                AxisTiling(TensorAxis(1), inner_partitions, inner_block, PADDING_ZERO))
+        return Layout(ORDER_BLOCK_MAJOR_TRANSPOSED,
+                      column_partitions * inner_partitions * copies, copies, axes, inner_block, 16)
+
+
+@dataclass(frozen=True)
+class TensorFormat:
+    """TensorFormat{precision, layout} (layout.rs:808-811)."""
+    precision: int
+    layout: Layout
+
+    def _c(self) -> _TensorFormat:
+        L = self.layout
+        if len(L.axes) > MAX_TILED_AXES:
+            raise ValueError(f"at most {MAX_TILED_AXES} tiled axes")
+        f = _TensorFormat(int(self.precision), int(L.order), int(L.row_block),
+                          int(L.column_block), int(L.tile_count), int(L.replicas), len(L.axes))
+        for i, a in enumerate(L.axes):
+            f.axes[i] = _AxisTiling(int(a.axis.from_end), int(a.axis.index), int(a.partitions),
+                                    int(a.padding_groups), int(a.block_size),
+                                    int(a.padding_multiple), int(a.shard_padding_multiple),
+                                    int(a.padding), int(a.tile_stride))
+        return f
 
 
 @dataclass(frozen=True)
@@ -695,6 +896,7 @@ class CompiledTensor:
     row_block: int
     column_block: int
     nbytes: int
+    shards: int = 1
 
     @property
     def dtype(self):
@@ -704,7 +906,8 @@ class CompiledTensor:
 def _tensor(info: _TensorInfo) -> CompiledTensor:
     return CompiledTensor(info.name.decode(), info.value,
                           tuple(info.dims[i] for i in range(info.rank)), info.precision,
-                          info.order, info.row_block, info.column_block, info.bytes)
+                          info.order, info.row_block, info.column_block, info.bytes,
+                          info.shards)
 
 
 class CompiledPackage:
@@ -758,8 +961,17 @@ class CompiledPackage:
 def build_package(graph: ComputeGraph, config: PackageConfig | None = None) -> CompiledPackage:
     """package.rs:532-538 for the GPU plan."""
     config = config or PackageConfig()
+    entries = [_InputFormat(int(v), 0, f._c()) for v, f in config.inputs.items()]
+    for v, prec in config.automatic_inputs.items():
+        fmt = _TensorFormat()
+        fmt.precision = int(prec)
+        fmt.order = ORDER_ROW_MAJOR
+        fmt.tile_count = fmt.replicas = 1
+        entries.append(_InputFormat(int(v), 1, fmt))
+    arr = (_InputFormat * max(1, len(entries)))(*entries)
     c = _PackageConfig(PRECISION_F32 if config.compute_precision == "f32" else PRECISION_F16,
-                       int(config.attention_output_f16))
+                       int(config.attention_output_f16), len(entries),
+                       ctypes.cast(arr, ctypes.POINTER(_InputFormat)))
     h = ctypes.c_void_p()
     _check(_lib().ipus_build_package(graph.handle, ctypes.byref(c), ctypes.byref(h)))
     return CompiledPackage(h.value)

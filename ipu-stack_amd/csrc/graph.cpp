@@ -32,6 +32,7 @@
 
 #include "internal.h"
 #include "kernels.h"
+#include "tiling.h"
 
 using namespace ipus;
 
@@ -549,7 +550,12 @@ struct Storage {
   int order = IPUS_ORDER_ROW_MAJOR;
   uint32_t row_block = 0, column_block = 0;
   Shape shape;
+  // A declared input format's host bytes (all shards, padding and replicas
+  // included); 0 for a plain tensor of `shape`.
+  uint64_t file_bytes = 0;
+  uint32_t shards = 1;
   uint64_t bytes() const {
+    if (file_bytes) return file_bytes;
     return elements(shape) * (precision == IPUS_PRECISION_F32 ? 4 : 2);
   }
 };
@@ -558,7 +564,10 @@ struct Storage {
 struct Slot {
   Storage storage;
   int first_def = -1, last_use = -1;
-  bool external = false;  // input or output binding
+  bool external = false;  // own buffer: input or output binding, or a constant
+  // Bytes uploaded into the slot's buffer when a session is created (the
+  // shard table of a declared input format).
+  std::vector<uint8_t> constant;
 };
 
 struct Operand {
@@ -1081,17 +1090,67 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
   if (!g || !out) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   *out = nullptr;
   if (!g->open.empty()) return build_error("graph has an open repeat body");
-  ipus_package_config cfg = {IPUS_PRECISION_F16, 0};
+  ipus_package_config cfg = {IPUS_PRECISION_F16, 0, 0, nullptr};
   if (config) cfg = *config;
   if (cfg.compute_precision != IPUS_PRECISION_F16 && cfg.compute_precision != IPUS_PRECISION_F32)
     return build_error("compute precision must be F16 or F32");
+  if (cfg.input_format_count < 0 || (cfg.input_format_count > 0 && !cfg.input_formats))
+    return build_error("input formats: bad count or null array");
+  // PipelineConfig inputs (config.rs:310-320): one entry per named input.
+  std::map<uint32_t, const ipus_input_format*> formats;
+  for (int i = 0; i < cfg.input_format_count; ++i) {
+    const ipus_input_format& f = cfg.input_formats[i];
+    bool is_input = false;
+    for (const auto& in : g->inputs) is_input = is_input || in.value == f.value;
+    if (!is_input)
+      return build_error("input format names value " + std::to_string(f.value) +
+                         ", which is not a graph input");
+    if (f.format.precision != IPUS_PRECISION_F16 && f.format.precision != IPUS_PRECISION_F32)
+      return build_error("input format precision must be F16 or F32");
+    formats[f.value] = &f;  // a later entry replaces an earlier one, as with_input does
+  }
   auto pkg = std::make_unique<ipus_package>();
   Builder b{*g, cfg, *pkg, {}};
   for (const auto& in : g->inputs) {
-    const int slot = b.new_slot(g->shapes.at(in.value), cfg.compute_precision);
+    const Shape& shape = g->shapes.at(in.value);
+    auto fit = formats.find(in.value);
+    const ipus_input_format* f = fit == formats.end() ? nullptr : fit->second;
+    const int precision = f ? f->format.precision : cfg.compute_precision;
+    const int slot = b.new_slot(shape, precision);
     pkg->slots[(size_t)slot].external = true;
     b.env[in.value] = slot;
     pkg->inputs.push_back({in.name, in.value, slot});
+    if (!f || f->automatic) continue;
+    // with_input: the host writes the format's shards; one unshard launch
+    // turns them into the row-major tensor the rest of the plan reads.
+    ipus::ResolvedFormat rf;
+    std::string error;
+    if (!ipus::resolve_format(shape, f->format, &rf, &error))
+      return build_error("input " + in.name + ": " + error);
+    if (ipus::format_is_row_major_identity(rf, f->format)) continue;
+    const uint64_t esize = precision == IPUS_PRECISION_F32 ? 4 : 2;
+    Storage& st = pkg->slots[(size_t)slot].storage;
+    st.order = f->format.order;
+    st.row_block = f->format.row_block;
+    st.column_block = f->format.column_block;
+    st.file_bytes = rf.file_elements * esize;
+    st.shards = f->format.tile_count;
+    uint32_t shard_count = 0;
+    uint64_t max_elements = 0;
+    const std::vector<uint32_t> table = ipus::shard_table(rf, &shard_count, &max_elements);
+    if (shard_count > 65535) return build_error("input " + in.name + ": too many shards");
+    if (st.file_bytes == 0 || shard_count == 0) continue;  // empty tensor: nothing to convert
+    const int tslot = b.new_slot({(uint32_t)(table.size() * 2)}, IPUS_PRECISION_F16);
+    Slot& ts = pkg->slots[(size_t)tslot];
+    ts.external = true;
+    ts.constant.resize(table.size() * 4);
+    memcpy(ts.constant.data(), table.data(), ts.constant.size());
+    const int out = b.new_slot(shape, precision);
+    b.emit("ipu_stack_unshard", out, {{slot, 0}, {tslot, 0}},
+           {shard_count, (uint32_t)shape.size(), (uint32_t)f->format.order, f->format.row_block,
+            f->format.column_block, (uint32_t)esize,
+            (uint32_t)std::min<uint64_t>(max_elements, 0xffffffffull)});
+    b.env[in.value] = out;
   }
   if (int e = b.lower_ops(g->root.operations)) return e;
   for (size_t i = 0; i < g->outputs.size(); ++i) {
@@ -1138,6 +1197,7 @@ int tensor_info(const ipus_package* p, const Binding& b, ipus_tensor_info* info)
   info->row_block = s.row_block;
   info->column_block = s.column_block;
   info->bytes = s.bytes();
+  info->shards = s.shards;
   return 0;
 }
 }  // namespace
@@ -1220,7 +1280,11 @@ extern "C" int ipus_session_create(ipus_context* ctx, const ipus_package* pkg, i
     const Slot& sl = pkg->slots[i];
     if (sl.external) {
       void* p = nullptr;
-      if (int e = ipus_buffer_alloc(ctx, sl.storage.bytes(), &p)) {
+      int e = ipus_buffer_alloc(ctx, sl.storage.bytes(), &p);
+      if (!e && !sl.constant.empty())
+        e = ipus_buffer_upload(ctx, p, sl.constant.data(), sl.constant.size());
+      if (e) {
+        if (p) ipus_buffer_free(ctx, p);
         for (void* q : s->owned) ipus_buffer_free(ctx, q);
         return e;
       }

@@ -572,6 +572,84 @@ __global__ __launch_bounds__(kThreads) void block_major_to_row_major_f16_kernel(
   for (int j = 0; j < 8; ++j) store16_nt(d + (uint64_t)(r0 + j) * columns + c0, out[j]);
 }
 
+// Unshard: host bytes of a declared input format (the shards of a tiled
+// tensor in logical tile order, each stored in an element order with zero
+// padding; package.rs:2101-2137, storage.rs:201-285) -> the row-major
+// logical tensor.  Workgroup row y handles table shard y; its threads walk
+// the shard's logical region in row-major order (so each thread's writes go
+// to consecutive destination elements of a row) and read each element at its
+// physical index inside the shard.  Element orders: IPUS_ORDER_* codes.
+// Table: kShardHeaderWords words (dims[8], reserved[8]), then per shard
+// 26 words: file element offset lo, hi, start[8], logical width[8],
+// physical width[8].
+constexpr uint32_t kUnshardHeader = 16, kUnshardShard = 26, kUnshardMaxRank = 8;
+
+__device__ __forceinline__ uint64_t shard_physical_index(uint32_t order, uint32_t rank,
+                                                         const uint32_t* c, const uint32_t* pw,
+                                                         uint32_t row_block,
+                                                         uint32_t column_block) {
+  if (order == 3) {  // row-major
+    uint64_t p = 0;
+    for (uint32_t a = 0; a < rank; ++a) p = p * pw[a] + c[a];
+    return p;
+  }
+  uint64_t outer = 0, outer_count = 1;
+  for (uint32_t a = 0; a + 2 < rank; ++a) {
+    outer = outer * pw[a] + c[a];
+    outer_count *= pw[a];
+  }
+  const uint32_t R = pw[rank - 2], C = pw[rank - 1], r = c[rank - 2], col = c[rank - 1];
+  const uint64_t matrix = outer * (uint64_t)R * C;
+  switch (order) {
+    case 0:  // AMP-Left: outer axes fold into the rows
+      return amp_left_index((uint32_t)(outer_count * R), (uint32_t)(outer * R + r), col);
+    case 4:  // AMP-Output
+      return amp_output_index((uint32_t)(outer_count * R), (uint32_t)(outer * R + r), col);
+    case 1:  // AMP-TransposedRight
+      return matrix + amp_transposed_right_index(R, C, r, col);
+    case 5:  // AMP-TransposedLeft
+      return matrix + amp_left_index(C, col, r);
+    case 6:  // AMP-TransposedOutput
+      return matrix + amp_output_index(C, col, r);
+    case 2:  // block-major Matrix
+      return matrix + block_major_index(row_block, column_block, C, r, col);
+    default:  // 7: block-major TransposedMatrix
+      return matrix + block_major_index(row_block, column_block, R, col, r);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void unshard_kernel(T* __restrict__ dst,
+                                                           const T* __restrict__ src,
+                                                           const uint32_t* __restrict__ table,
+                                                           uint32_t rank, uint32_t order,
+                                                           uint32_t row_block,
+                                                           uint32_t column_block) {
+  const uint32_t* sh = table + kUnshardHeader + (uint64_t)blockIdx.y * kUnshardShard;
+  const uint64_t offset = (uint64_t)sh[0] | ((uint64_t)sh[1] << 32);
+  uint32_t dims[kUnshardMaxRank], start[kUnshardMaxRank], lw[kUnshardMaxRank],
+      pw[kUnshardMaxRank], c[kUnshardMaxRank];
+  uint64_t n = 1;
+  for (uint32_t a = 0; a < rank; ++a) {
+    dims[a] = table[a];
+    start[a] = sh[2 + a];
+    lw[a] = sh[2 + kUnshardMaxRank + a];
+    pw[a] = sh[2 + 2 * kUnshardMaxRank + a];
+    n *= lw[a];
+  }
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    uint64_t rem = i;
+    for (int a = (int)rank - 1; a >= 0; --a) {
+      c[a] = (uint32_t)(rem % lw[a]);
+      rem /= lw[a];
+    }
+    uint64_t d = 0;
+    for (uint32_t a = 0; a < rank; ++a) d = d * dims[a] + start[a] + c[a];
+    dst[d] = src[offset + shard_physical_index(order, rank, c, pw, row_block, column_block)];
+  }
+}
+
 // Grid for a grid-stride kernel: one work item per thread up to 2^24
 // workgroups.  A one-shot grid keeps every wave's loads independent (a
 // 256 MiB copy: 5.7 TB/s with 2,048 workgroups looping, 6.5 one-shot).
@@ -774,6 +852,26 @@ int launch_split_heads(hipStream_t stream, void* dst, const void* src, uint32_t 
                        stream, (uint32_t*)dst, (const uint32_t*)src, rows, heads, channels, total);
   else
     return IPUS_ERROR_INVALID_ARGUMENT;
+  return hip_status(hipGetLastError());
+}
+
+int launch_unshard(hipStream_t stream, void* dst, const void* src, const void* table,
+                   uint32_t shards, uint32_t rank, uint32_t order, uint32_t row_block,
+                   uint32_t column_block, uint32_t element_bytes, uint32_t max_shard_elements) {
+  if (shards == 0 || max_shard_elements == 0) return 0;
+  if (rank == 0 || rank > kUnshardMaxRank || order > 7 || shards > 65535 ||
+      (element_bytes != 2 && element_bytes != 4) || (order != 3 && element_bytes != 2) ||
+      ((order == 2 || order == 7) && (row_block == 0 || column_block == 0 || row_block % kMicro)))
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  const dim3 grid(grid_for(max_shard_elements, 4096), shards);
+  if (element_bytes == 2)
+    hipLaunchKernelGGL(unshard_kernel<uint16_t>, grid, dim3(kThreads), 0, stream, (uint16_t*)dst,
+                       (const uint16_t*)src, (const uint32_t*)table, rank, order, row_block,
+                       column_block);
+  else
+    hipLaunchKernelGGL(unshard_kernel<uint32_t>, grid, dim3(kThreads), 0, stream, (uint32_t*)dst,
+                       (const uint32_t*)src, (const uint32_t*)table, rank, order, row_block,
+                       column_block);
   return hip_status(hipGetLastError());
 }
 

@@ -45,6 +45,12 @@ int gemm_f16_split_chunk(uint32_t inner, uint32_t splits);
 int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits);
 int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
                              uint64_t count, bool gelu);
+// Declared input format -> row-major (k_memory.hip): `table` is the shard
+// table of tiling.h in device memory; one workgroup row per table shard,
+// `max_shard_elements` sizes the grid.
+int launch_unshard(hipStream_t stream, void* dst, const void* src, const void* table,
+                   uint32_t shards, uint32_t rank, uint32_t order, uint32_t row_block,
+                   uint32_t column_block, uint32_t element_bytes, uint32_t max_shard_elements);
 // Split-K with the partials in the library's per-device scratch array
 // (no allocation): split_scratch_init(device) looks up the device's copy
 // once, with that device current; the launch then runs the split GEMM into

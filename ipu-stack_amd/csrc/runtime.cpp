@@ -508,6 +508,15 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_to_row_major_f16(c->stream, o, i[0], s[0], s[1], s[2], s[3], s[4], s[5]);
        }},
+      // Declared input format -> row-major: input 0 the host bytes (the
+      // shards in tile order), input 1 the shard table (tiling.h).
+      {"ipu_stack_unshard", 2,
+       {"shards", "rank", "order", "row_block", "column_block", "element_bytes",
+        "max_shard_elements"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_unshard(c->stream, o, i[0], i[1], s[0], s[1], s[2], s[3], s[4], s[5],
+                               s[6]);
+       }},
       {"ipus_gelu_f16", 1, {"element_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_gelu_f16(c->stream, o, i[0], s[0]);

@@ -403,6 +403,69 @@ int or_unpack_to_row_major_f16(int source_order, uint32_t matrices,
   return 0;
 }
 
+/*
+ * One shard of a tiled binding: storage.rs:201-285 (physical_index over the
+ * shard's physical widths: row-major; block-major matrices matrix-major over
+ * the outer axes; AMP Left / Output with the outer axes folded into the
+ * rows; the transposed AMP roles matrix-major).
+ */
+int or_pack_shard(int kind, int variant, uint32_t row_block, uint32_t column_block,
+                  int rank, const uint32_t *dims, const uint32_t *start,
+                  const uint32_t *logical_end, const uint32_t *physical_end,
+                  const uint16_t *logical, uint16_t *shard) {
+  if (rank < 1 || rank > 8) return -1;
+  if (kind != 0 && rank < 2) return -1;
+  uint32_t w[8], lw[8], c[8];
+  uint64_t total = 1, logical_total = 1;
+  for (int a = 0; a < rank; ++a) {
+    w[a] = physical_end[a] - start[a];
+    lw[a] = logical_end[a] - start[a];
+    total *= w[a];
+    logical_total *= lw[a];
+  }
+  for (uint64_t i = 0; i < logical_total; ++i) {
+    uint64_t rem = i;
+    for (int a = rank - 1; a >= 0; --a) {
+      c[a] = (uint32_t)(rem % lw[a]);
+      rem /= lw[a];
+    }
+    uint64_t src = 0;
+    for (int a = 0; a < rank; ++a) src = src * dims[a] + start[a] + c[a];
+    int64_t phys;
+    if (kind == 0) {
+      uint64_t p = 0;
+      for (int a = 0; a < rank; ++a) p = p * w[a] + c[a];
+      phys = (int64_t)p;
+    } else {
+      uint64_t outer = 0, outer_count = 1;
+      for (int a = 0; a + 2 < rank; ++a) {
+        outer = outer * w[a] + c[a];
+        outer_count *= w[a];
+      }
+      const uint32_t R = w[rank - 2], C = w[rank - 1];
+      const uint32_t r = c[rank - 2], col = c[rank - 1];
+      const uint64_t matrix = outer * (uint64_t)R * C;
+      if (kind == 2) {
+        const int64_t within = or_block_major_matrix_index(variant, row_block, column_block,
+                                                           OR_F16, R, C, r, col);
+        if (within < 0) return -2;
+        phys = (int64_t)matrix + within;
+      } else if (variant == OR_AMP_LEFT || variant == OR_AMP_OUTPUT) {
+        phys = or_amp_matrix_index(variant, OR_F16, (uint32_t)(outer_count * R), C,
+                                   (uint32_t)(outer * R + r), col);
+        if (phys < 0) return -2;
+      } else {
+        const int64_t within = or_amp_matrix_index(variant, OR_F16, R, C, r, col);
+        if (within < 0) return -2;
+        phys = (int64_t)matrix + within;
+      }
+    }
+    if (phys < 0 || (uint64_t)phys >= total) return -3;
+    shard[phys] = logical[src];
+  }
+  return 0;
+}
+
 /* Plain transpose: row-major [rows, columns] -> row-major [columns, rows]. */
 void or_transpose_u16(uint32_t matrices, uint32_t rows, uint32_t columns,
                       const uint16_t *src, uint16_t *dst) {

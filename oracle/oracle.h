@@ -57,6 +57,18 @@ int or_block_major_matrix_coordinates(int transposed, uint32_t row_block,
                                       uint32_t linear, uint32_t *row,
                                       uint32_t *column);
 
+/* ---- one shard of a tiled host binding, storage.rs:201-299
+ * (physical_index) and package.rs:2101-2137 (shard bytes) ----
+ * kind 0 row-major, 1 AMP (`variant` = AmpOrder role above), 2 block-major
+ * (`variant` = 1 for TransposedMatrix).  The shard covers [start, logical_end)
+ * of each of `rank` axes of a row-major logical tensor `dims`, stored with
+ * physical widths physical_end - start; padding elements stay as the caller
+ * left them (zero).  Returns 0, or < 0 when an index is invalid. */
+int or_pack_shard(int kind, int variant, uint32_t row_block, uint32_t column_block,
+                  int rank, const uint32_t *dims, const uint32_t *start,
+                  const uint32_t *logical_end, const uint32_t *physical_end,
+                  const uint16_t *logical, uint16_t *shard);
+
 /* ---- rearrange / unpack kernels (device/rearrange_f16.cpp,
  *      device/unpack_amp_f16.cpp) on 16-bit payloads ---- */
 int or_rearrange_row_major_f16(int target_order, uint32_t row_block,

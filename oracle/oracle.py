@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
             "or_reduce_rows_f16": (None, [P, u32, u32, P, i32]),
             "or_reduce_rows_block_major_f16": (i32, [P, u32, u32, u32, u32, P, i32]),
             "or_splitmix64": (u64, [u64]),
+            "or_pack_shard": (i32, [i32, i32, u32, u32, i32, P, P, P, P, P, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(_lib, name)
@@ -273,3 +274,124 @@ def reduce_rows_block_major_f16(src, row_block, column_block, rows, columns,
 
 def splitmix64(state: int) -> int:
     return lib().or_splitmix64(state)
+
+
+# ---- tiled host bindings (crates/ipu-codegen/src/layout.rs, storage.rs) ----
+def _axis_defaults(a: dict) -> dict:
+    """AxisTiling::new defaults (layout.rs:169-179) for missing fields."""
+    d = dict(a)
+    d.setdefault("padding_groups", 1)
+    d.setdefault("padding_multiple", d["block_size"])
+    d.setdefault("shard_padding_multiple", 1)
+    d.setdefault("zero_padding", False)
+    d.setdefault("tile_stride", None)
+    return d
+
+
+def _axis_bounds(a: dict, padded_extent: int, logical_extent: int, coordinate: int):
+    """resolve_axis_bounds, layout.rs:1427-1504: (start, logical_end,
+    physical_end) of partition `coordinate`."""
+    partitions, groups = a["partitions"], a["padding_groups"]
+    per_group = partitions // groups
+    group, in_group = divmod(coordinate, per_group)
+    padded_group = padded_extent // groups
+    logical_group = logical_extent // groups
+    if padded_group % a["block_size"]:
+        raise ValueError("indivisible axis")
+    blocks = padded_group // a["block_size"]
+    short, long_shards = divmod(blocks, per_group)
+    start_blocks = in_group * short + min(in_group, long_shards)
+    shard_blocks = short + (1 if in_group < long_shards else 0)
+    start_in_group = start_blocks * a["block_size"]
+    allocated = shard_blocks * a["block_size"]
+    rem = allocated % a["shard_padding_multiple"]
+    if rem and not a["zero_padding"]:
+        raise ValueError("indivisible shard")
+    width = allocated + (a["shard_padding_multiple"] - rem if rem else 0)
+    base = group * logical_group
+    start = base + start_in_group
+    logical_end = base + max(min(start_in_group + allocated, logical_group), start_in_group)
+    return start, logical_end, start + width
+
+
+def resolve_tiling(shape, tile_count: int, replicas: int, axes) -> list:
+    """Per tile, in logical tile order, the (start, logical_end,
+    physical_end) of every axis: ResolvedLayout::resolve and shard_extents
+    (layout.rs:1002-1135, 1267-1300).  `axes` are dicts with AxisTiling's
+    fields (`axis` as ("end", k) or ("start", k))."""
+    rank = len(shape)
+    padded = list(shape)
+    resolved = []
+    used = replicas
+    for raw in axes:
+        a = _axis_defaults(raw)
+        kind, k = a["axis"]
+        index = rank - k if kind == "end" else k
+        if not (0 <= index < rank) or (kind == "end" and k == 0):
+            raise ValueError("axis out of range")
+        if any(r["index"] == index for r in resolved):
+            raise ValueError("duplicate axis")
+        used *= a["partitions"]
+        extent = padded[index]
+        if a["partitions"] % a["padding_groups"] or extent % a["padding_groups"]:
+            raise ValueError("invalid padding groups")
+        group_extent = extent // a["padding_groups"]
+        rem = group_extent % a["padding_multiple"]
+        if rem and not a["zero_padding"]:
+            raise ValueError("indivisible axis")
+        if rem:
+            padded[index] = (group_extent + a["padding_multiple"] - rem) * a["padding_groups"]
+        if (padded[index] // a["padding_groups"]) % a["block_size"]:
+            raise ValueError("indivisible axis")
+        a["index"] = index
+        resolved.append(a)
+    if used != tile_count:
+        raise ValueError("tile count mismatch")
+    packed = replicas
+    for a in resolved:                       # axis_strides, layout.rs:234-251
+        a["stride"] = a["tile_stride"] or packed
+        packed *= a["partitions"]
+    tiles = []
+    for tile in range(tile_count):
+        ext = [(0, shape[i], padded[i]) for i in range(rank)]
+        for a in resolved:
+            c = (tile // a["stride"]) % a["partitions"]
+            ext[a["index"]] = _axis_bounds(a, padded[a["index"]], shape[a["index"]], c)
+        tiles.append(ext)
+    return tiles
+
+
+ORDER_ROW_MAJOR, ORDER_AMP, ORDER_BLOCK_MAJOR = 0, 1, 2
+
+
+def pack_tiled(logical, shape, kind: int, variant: int, tile_count: int, replicas: int, axes,
+               row_block: int = 0, column_block: int = 0) -> np.ndarray:
+    """The host bytes of a tiled binding (CompiledTensor::binding,
+    package.rs:2101-2137): every tile's shard in logical tile order, each of
+    its physical widths, the logical elements placed by storage.rs's
+    physical_index and the padding zero.  kind 0 row-major (any dtype), 1 AMP
+    (variant = AmpOrder role), 2 block-major (variant 1 = TransposedMatrix;
+    fp16 only for kinds 1 and 2)."""
+    x = np.ascontiguousarray(logical).reshape(shape)
+    pieces = []
+    for ext in resolve_tiling(list(shape), tile_count, replicas, axes):
+        widths = [pe - st for st, _, pe in ext]
+        shard = np.zeros(widths, dtype=x.dtype)
+        if kind == ORDER_ROW_MAJOR:
+            region = tuple(slice(st, le) for st, le, _ in ext)
+            shard[tuple(slice(0, le - st) for st, le, _ in ext)] = x[region]
+        else:
+            if x.dtype != np.uint16:
+                raise ValueError("AMP and block-major packing is fp16 only")
+            rank = len(shape)
+            arr = lambda v: (ctypes.c_uint32 * rank)(*v)  # noqa: E731
+            flat = shard.reshape(-1)
+            src = x.reshape(-1)
+            status = lib().or_pack_shard(kind, variant, row_block, column_block, rank,
+                                         arr(shape), arr([e[0] for e in ext]),
+                                         arr([e[1] for e in ext]), arr([e[2] for e in ext]),
+                                         src.ctypes.data, flat.ctypes.data)
+            if status != 0:
+                raise ValueError(f"oracle pack_shard rejected the shard ({status})")
+        pieces.append(shard.reshape(-1))
+    return np.concatenate(pieces) if pieces else np.zeros(0, dtype=x.dtype)

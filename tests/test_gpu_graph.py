@@ -360,3 +360,124 @@ def test_injected_launch_failure_propagates_and_releases_everything(ipus, oracle
     assert s2.handle is None and extra.ptr == 0
     with pytest.raises(ipus.IpusError):
         s2.run()
+
+
+# ---------------------------------------------------------------------------
+# Declared input formats: reference-layout bytes in, row-major results out
+# ---------------------------------------------------------------------------
+from test_graph import FORMAT_CASES, oracle_layout_args  # noqa: E402
+
+
+@pytest.mark.parametrize("name,shape,make", FORMAT_CASES, ids=[c[0] for c in FORMAT_CASES])
+def test_declared_format_unshards_bit_exact(ipus, oracle, ctx, name, shape, make):
+    """Every layout of the CPU plan tests: the oracle packs random fp16 data
+    into the format's host bytes, the package's unshard launch rebuilds the
+    tensor, which the graph returns unchanged (bit-exact)."""
+    layout = make(ipus.Layout)
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", shape)
+    g.set_outputs([x])
+    cfg = ipus.PackageConfig().with_input(x, ipus.TensorFormat(ipus.PRECISION_F16, layout))
+    n = int(np.prod(shape))
+    data = synth(ipus, n, 71, len(name))
+    packed = oracle.pack_tiled(data, shape, **oracle_layout_args(ipus, layout))
+    pkg, (y,) = run_package(ipus, ctx, g, {"x": packed}, cfg)
+    assert "ipu_stack_unshard" in [s[0] for s in pkg.steps]
+    assert np.array_equal(y.reshape(-1), data)
+
+
+@pytest.mark.parametrize("batch,tiles", [(1, 8), (3, 8), (3, 5)])
+def test_reference_gemm_smoke_from_reference_layout_bytes(ipus, oracle, ctx, batch, tiles):
+    """The reference's GEMM smoke graph (crates/ipu-tests/src/main.rs:595-613):
+    left [batch, tiles, 64] in amp_left(64, tiles), right [1, 64, 64 tiles] in
+    block_major_matrix(64, tiles), bytes built as run_gemm builds them
+    (one-hot left selecting inner (7 b + t) % 64, right = gemm_right_value,
+    main.rs:1079-1105, 2133-2136).  Every output is exact."""
+    L = ipus.Layout
+    g = ipus.ComputeGraph()
+    left = g.host_input("left", [batch, tiles, 64])
+    right = g.parameter("right", [1, 64, tiles * 64])
+    g.set_outputs([g.gemm(left, right)])
+    lf, rf = L.amp_left(64, tiles), L.block_major_matrix(64, tiles)
+    cfg = (ipus.PackageConfig()
+           .with_input(left, ipus.TensorFormat(ipus.PRECISION_F16, lf))
+           .with_input(right, ipus.TensorFormat(ipus.PRECISION_F16, rf)))
+    levels = np.array([0xBC00, 0xB800, 0x0000, 0x3800, 0x3C00], dtype=np.uint16)
+    b, t = np.meshgrid(np.arange(batch), np.arange(tiles), indexing="ij")
+    selected = (b * 7 + t) % 64
+    lx = np.zeros((batch, tiles, 64), dtype=np.uint16)
+    lx[b, t, selected] = 0x3C00
+    inner, col = np.meshgrid(np.arange(64), np.arange(tiles * 64), indexing="ij")
+    rx = levels[(inner * 3 + col) % 5].reshape(1, 64, tiles * 64)
+    feeds = {"left": oracle.pack_tiled(lx, lx.shape, **oracle_layout_args(ipus, lf)),
+             "right": oracle.pack_tiled(rx, rx.shape, **oracle_layout_args(ipus, rf))}
+    pkg, (y,) = run_package(ipus, ctx, g, feeds, cfg)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_unshard", "ipu_stack_unshard",
+                                         "ipu_stack_gemm_f16"]
+    want = rx[0][selected]                               # [batch, tiles, 64 tiles]
+    assert np.array_equal(y.reshape(batch, tiles, tiles * 64), want)
+
+
+def test_reference_mlp_smoke_from_reference_layout_bytes(ipus, oracle, ctx):
+    """The reference's MLP smoke (main.rs:614-634): left [tiles, 64] in
+    amp_left(64, tiles), both [64, 64] weights in block_major_matrix(64,
+    tiles) (tile 0 holds the whole weight, the other slices are empty),
+    GEMM -> GELU -> GEMM -> GELU; checked against the oracle at the fp16 bar
+    and the reference's own 0.02 bound (main.rs:1929-2033)."""
+    tiles = 16
+    L = ipus.Layout
+    g = ipus.ComputeGraph()
+    left = g.host_input("left", [tiles, 64])
+    r0 = g.parameter("right.0", [64, 64])
+    r1 = g.parameter("right.1", [64, 64])
+    g.set_outputs([g.gelu(g.gemm(g.gelu(g.gemm(left, r0)), r1))])
+    lf, rf = L.amp_left(64, tiles), L.block_major_matrix(64, tiles)
+    cfg = (ipus.PackageConfig().with_input(left, ipus.TensorFormat(ipus.PRECISION_F16, lf))
+           .with_input(r0, ipus.TensorFormat(ipus.PRECISION_F16, rf))
+           .with_input(r1, ipus.TensorFormat(ipus.PRECISION_F16, rf)))
+    x = synth(ipus, tiles * 64, 72, 1, scale=1.0)
+    w0 = synth(ipus, 64 * 64, 72, 2, scale=0.125)
+    w1 = synth(ipus, 64 * 64, 72, 3, scale=0.125)
+    args_l, args_r = oracle_layout_args(ipus, lf), oracle_layout_args(ipus, rf)
+    feeds = {"left": oracle.pack_tiled(x, [tiles, 64], **args_l),
+             "right.0": oracle.pack_tiled(w0, [64, 64], **args_r),
+             "right.1": oracle.pack_tiled(w1, [64, 64], **args_r)}
+    assert feeds["right.0"].size == 64 * 64            # 15 empty slices
+    pkg, (y,) = run_package(ipus, ctx, g, feeds, cfg)
+    h = oracle.gelu_f16(oracle.gemm_f16(x, w0, tiles, 64, 64))
+    want = oracle.f16_to_f32(oracle.gelu_f16(oracle.gemm_f16(h, w1, tiles, 64, 64)))
+    got = oracle.f16_to_f32(y).reshape(-1)
+    assert fp16_close(got, want, FP16_TOL)
+    assert np.max(np.abs(got - want)) <= 0.02
+
+
+def test_reference_attention_smoke_from_reference_layout_bytes(ipus, oracle, ctx):
+    """The reference's attention smoke (main.rs:671-701, 1305-1505): Q
+    [4, 17, 72] in attention_output(4, query_partitions), K and V [4, 19, 72]
+    in attention_output(4, 1), N(0, 0.25); the fp32 output within the
+    smoke's max 0.012 and rms 0.003 of the oracle."""
+    heads, qr, kr, d = 4, 17, 19, 72
+    active_tiles = 64
+    qparts = min(qr, active_tiles // heads)
+    kparts = -(-kr // 64)
+    L = ipus.Layout
+    g = ipus.ComputeGraph()
+    q = g.host_input("query", [heads, qr, d])
+    k = g.host_input("key", [heads, kr, d])
+    v = g.host_input("value", [heads, kr, d])
+    g.set_outputs([g.flash_attention(q, k, v)])
+    qf, kf = L.attention_output(heads, qparts), L.attention_output(heads, kparts)
+    cfg = (ipus.PackageConfig().with_input(q, ipus.TensorFormat(ipus.PRECISION_F16, qf))
+           .with_input(k, ipus.TensorFormat(ipus.PRECISION_F16, kf))
+           .with_input(v, ipus.TensorFormat(ipus.PRECISION_F16, kf)))
+    qs = synth(ipus, heads * qr * d, 73, 1, scale=0.25)
+    ks = synth(ipus, heads * kr * d, 73, 2, scale=0.25)
+    vs = synth(ipus, heads * kr * d, 73, 3, scale=0.25)
+    feeds = {"query": oracle.pack_tiled(qs, [heads, qr, d], **oracle_layout_args(ipus, qf)),
+             "key": oracle.pack_tiled(ks, [heads, kr, d], **oracle_layout_args(ipus, kf)),
+             "value": oracle.pack_tiled(vs, [heads, kr, d], **oracle_layout_args(ipus, kf))}
+    pkg, (y,) = run_package(ipus, ctx, g, feeds, cfg)
+    want = oracle.attention(oracle.f16_to_f32(qs), oracle.f16_to_f32(ks), oracle.f16_to_f32(vs),
+                            heads, qr, kr, d, d)
+    err = np.abs(y.reshape(-1) - want.reshape(-1))
+    assert float(err.max()) <= 0.012 and float(np.sqrt(np.mean(err ** 2))) <= 0.003

@@ -8,6 +8,7 @@ from __future__ import annotations
 import math
 import random
 
+import numpy as np
 import pytest
 
 RANDOM_CASES = 256
@@ -450,3 +451,123 @@ def test_build_package_batched_gemm_with_u32_overflowing_stride(ipus):
     pkg = ipus.build_package(g)
     gemms = [s for s in pkg.steps if s[0] == "ipu_stack_gemm_f16"]
     assert len(gemms) == 2 and all(s[2][0] == 1 and s[2][6] == 0 for s in gemms)
+
+
+# ---------------------------------------------------------------------------
+# Declared input formats (PipelineConfig::with_input, config.rs:310-320)
+# ---------------------------------------------------------------------------
+def oracle_layout_args(ipus, layout):
+    """The oracle's packer arguments for a product Layout (test glue)."""
+    kinds = {ipus.ORDER_ROW_MAJOR: (0, 0), ipus.ORDER_AMP_LEFT: (1, 0),
+             ipus.ORDER_AMP_TRANSPOSED_LEFT: (1, 1), ipus.ORDER_AMP_TRANSPOSED_RIGHT: (1, 2),
+             ipus.ORDER_AMP_OUTPUT: (1, 3), ipus.ORDER_AMP_TRANSPOSED_OUTPUT: (1, 4),
+             ipus.ORDER_BLOCK_MAJOR: (2, 0), ipus.ORDER_BLOCK_MAJOR_TRANSPOSED: (2, 1)}
+    kind, variant = kinds[layout.order]
+    axes = [dict(axis=("end" if a.axis.from_end else "start", a.axis.index),
+                 partitions=a.partitions, block_size=a.block_size,
+                 padding_groups=a.padding_groups,
+                 padding_multiple=a.padding_multiple or a.block_size,
+                 shard_padding_multiple=a.shard_padding_multiple,
+                 zero_padding=a.padding == ipus.PADDING_ZERO,
+                 tile_stride=a.tile_stride or None) for a in layout.axes]
+    return dict(kind=kind, variant=variant, tile_count=layout.tile_count,
+                replicas=layout.replicas, axes=axes, row_block=layout.row_block,
+                column_block=layout.column_block)
+
+
+FORMAT_CASES = [
+    ("amp_left", [3, 4, 64], lambda L: L.amp_left(64, 4)),
+    ("amp_left_padded", [2, 5, 40], lambda L: L.amp_left(64, 5)),
+    ("block_major", [1, 64, 256], lambda L: L.block_major_matrix(64, 4)),
+    ("block_major_empty_shards", [64, 64], lambda L: L.block_major_matrix(64, 4)),
+    ("attention_output", [4, 17, 72], lambda L: L.attention_output(4, 5)),
+    ("attention_key", [4, 19, 72], lambda L: L.attention_key(4, 1)),
+    ("attention_query", [4, 17, 72], lambda L: L.attention_query(4, 3)),
+    ("attention_block_major_kv", [4, 130, 72], lambda L: L.attention_block_major_key_value(4, 3)),
+    ("amp_output", [6, 40], lambda L: L.amp_output(3)),
+    ("transposed_block_major", [100, 64], lambda L: L.transposed_block_major_matrix_storage(
+        64, 64, 2, 1, 1)),
+    ("block_major_copies", [64, 128], lambda L: L.block_major_matrix_storage(64, 64, 2, 1, 2)),
+]
+
+
+@pytest.mark.parametrize("name,shape,make", FORMAT_CASES, ids=[c[0] for c in FORMAT_CASES])
+def test_declared_input_format_plans_one_unshard(ipus, oracle, name, shape, make):
+    """A with_input format makes the input binding hold the shards' bytes
+    (the oracle's packing of the same layout has the same size) and plans
+    one ipu_stack_unshard step ahead of the consumer."""
+    layout = make(ipus.Layout)
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", shape)
+    g.set_outputs([g.gelu(x)])
+    cfg = ipus.PackageConfig().with_input(x, ipus.TensorFormat(ipus.PRECISION_F16, layout))
+    pkg = ipus.build_package(g, cfg)
+    n = int(np.prod(shape))
+    packed = oracle.pack_tiled(np.ones(n, np.uint16), shape, **oracle_layout_args(ipus, layout))
+    assert pkg.inputs[0].nbytes == packed.nbytes
+    assert pkg.inputs[0].shards == layout.tile_count
+    assert [s[0] for s in pkg.steps][:2] == ["ipu_stack_unshard", "ipu_stack_gelu_tanh_approx_f16"]
+
+
+def test_declared_row_major_identity_needs_no_conversion(ipus):
+    """Row-sharded row-major data without padding is already the tensor."""
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [8, 64])
+    g.set_outputs([g.gelu(x)])
+    cfg = ipus.PackageConfig().with_input(
+        x, ipus.TensorFormat(ipus.PRECISION_F16, ipus.Layout.row_sharded(4)))
+    pkg = ipus.build_package(g, cfg)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gelu_tanh_approx_f16"]
+    assert pkg.inputs[0].nbytes == 8 * 64 * 2
+
+
+def test_automatic_input_fixes_precision_and_casts(ipus):
+    """with_automatic_input(value, F32): the host writes fp32 row-major and
+    the plan casts to the fp16 compute precision."""
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [64, 64])
+    w = g.parameter("w", [64, 64])
+    g.set_outputs([g.gemm(x, w)])
+    cfg = ipus.PackageConfig().with_automatic_input(x, ipus.PRECISION_F32)
+    pkg = ipus.build_package(g, cfg)
+    assert pkg.inputs[0].precision == ipus.PRECISION_F32 and pkg.inputs[0].nbytes == 64 * 64 * 4
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_cast_f32_f16", "ipu_stack_gemm_f16"]
+
+
+@pytest.mark.parametrize("shape,make,message", [
+    ([4, 40], lambda L: L.row_major(2, [ipus_axis(1, 2, 16)]), "multiple"),  # Reject, 40 % 16
+    ([3, 4, 64], lambda L: replace_tiles(L.amp_left(64, 4), 5), "tile count"),
+    ([4, 64], lambda L: L.row_major(4, [ipus_axis(2, 2, 1).with_tile_stride(1),
+                                        ipus_axis(1, 2, 1).with_tile_stride(1)]), "strides"),
+])
+def test_declared_input_format_errors(ipus, shape, make, message):
+    import re
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", shape)
+    g.set_outputs([g.gelu(x)])
+    cfg = ipus.PackageConfig().with_input(x, ipus.TensorFormat(ipus.PRECISION_F16,
+                                                               make(ipus.Layout)))
+    with pytest.raises(ipus.PackageBuildError) as err:
+        ipus.build_package(g, cfg)
+    assert re.search(message, err.value.message)
+
+
+def ipus_axis(from_end, partitions, block):
+    import importlib
+    m = importlib.import_module("ipu_stack_amd")
+    return m.AxisTiling(m.TensorAxis(from_end), partitions, block)
+
+
+def replace_tiles(layout, tiles):
+    import dataclasses
+    return dataclasses.replace(layout, tile_count=tiles)
+
+
+def test_input_format_for_a_non_input_is_rejected(ipus):
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [16, 16])
+    y = g.gelu(x)
+    g.set_outputs([y])
+    cfg = ipus.PackageConfig().with_automatic_input(y, ipus.PRECISION_F16)
+    with pytest.raises(ipus.PackageBuildError):
+        ipus.build_package(g, cfg)

@@ -481,3 +481,120 @@ def test_golden_fixtures(oracle):
     # tanh-GELU at fixed points (float64 closed form at generation time)
     got = np.array([oracle.gelu_reference(float(x)) for x in data["gelu_x"]])
     assert np.allclose(got, data["gelu_y"], rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# Tiled host bindings: the oracle's packer against the byte construction of
+# the reference's own hardware tests (crates/ipu-tests/src/main.rs), which
+# fill each tile's slice element by element from the layout's coordinates.
+# ---------------------------------------------------------------------------
+def _amp_left(tiles, inner=64):
+    """Layout::amp_left(inner, tiles) (layout.rs:376-389)."""
+    return [dict(axis=("end", 2), partitions=tiles, block_size=1),
+            dict(axis=("end", 1), partitions=1, block_size=inner, zero_padding=True)]
+
+
+def _block_major_matrix(row_block, tiles):
+    """Layout::block_major_matrix -> block_major_matrix_storage(row_block, 64,
+    tiles, 1, 1) (layout.rs:391-400, 552-590)."""
+    return [dict(axis=("end", 1), partitions=tiles, block_size=64, zero_padding=True,
+                 tile_stride=1),
+            dict(axis=("end", 2), partitions=1, block_size=row_block, zero_padding=True)]
+
+
+def _attention_output(heads, parts):
+    """Layout::attention_output (layout.rs:305-316, 367-375)."""
+    return [dict(axis=("end", 2), partitions=parts, block_size=1, tile_stride=heads),
+            dict(axis=("end", 3), partitions=heads, block_size=1, tile_stride=1),
+            dict(axis=("end", 1), partitions=1, block_size=16, zero_padding=True)]
+
+
+@pytest.mark.parametrize("batch,tiles", [(1, 4), (3, 4), (3, 7)])
+def test_pack_gemm_smoke_left_matches_run_gemm(oracle, batch, tiles):
+    """main.rs:1079-1089: tile t's slice holds batch x 64 elements whose
+    (batch_index, inner) = amp_matrix_coordinates(Left, F16, batch, 64,
+    linear) is logical element [batch_index, t, inner]; slices follow in tile
+    order (package.rs:2112-2128)."""
+    x = (np.arange(batch * tiles * 64, dtype=np.uint32) % 65000 + 1).astype(np.uint16)
+    got = oracle.pack_tiled(x, [batch, tiles, 64], 1, oracle.AMP_LEFT, tiles, 1, _amp_left(tiles))
+    x3 = x.reshape(batch, tiles, 64)
+    slice_elements = batch * 64
+    assert got.size == tiles * slice_elements
+    for t in range(tiles):
+        for linear in range(slice_elements):
+            b, inner = oracle.amp_matrix_coordinates(oracle.AMP_LEFT, oracle.F16, batch, 64, linear)
+            assert got[t * slice_elements + linear] == x3[b, t, inner]
+
+
+@pytest.mark.parametrize("tiles", [1, 3])
+def test_pack_gemm_smoke_right_matches_run_gemm(oracle, tiles):
+    """main.rs:1090-1105: tile t's slice is the 64 x 64 column block t in
+    block-major {64, 16}: (inner, column) = block_major_matrix_coordinates(
+    Matrix{64, 16}, F16, 64, 64, linear) is logical [0, inner, 64 t + column]."""
+    x = (np.arange(64 * tiles * 64, dtype=np.uint32) % 65000 + 1).astype(np.uint16)
+    got = oracle.pack_tiled(x, [1, 64, tiles * 64], 2, 0, tiles, 1, _block_major_matrix(64, tiles),
+                            64, 16)
+    x3 = x.reshape(1, 64, tiles * 64)
+    assert got.size == tiles * 4096
+    for t in range(tiles):
+        for linear in range(4096):
+            inner, col = oracle.block_major_matrix_coordinates(0, 64, 16, oracle.F16, 64, 64,
+                                                               linear)
+            assert got[t * 4096 + linear] == x3[0, inner, t * 64 + col]
+
+
+def test_pack_mlp_smoke_weights_leave_empty_shards(oracle):
+    """main.rs:1146-1166: a [64, 64] weight in block_major_matrix(64, tiles)
+    has one 64-column block, so tile 0 holds it all and the other tiles'
+    slices are empty."""
+    tiles = 4
+    x = (np.arange(4096, dtype=np.uint32) + 1).astype(np.uint16)
+    got = oracle.pack_tiled(x, [64, 64], 2, 0, tiles, 1, _block_major_matrix(64, tiles), 64, 16)
+    assert got.size == 4096
+    for linear in range(4096):
+        inner, col = oracle.block_major_matrix_coordinates(0, 64, 16, oracle.F16, 64, 64, linear)
+        assert got[linear] == x[inner * 64 + col]
+
+
+def _balanced_range(extent, partitions, partition):
+    """main.rs:1507-1512."""
+    base, rem = divmod(extent, partitions)
+    return partition * base + min(partition, rem), base + (1 if partition < rem else 0)
+
+
+@pytest.mark.parametrize("heads,rows,parts", [(4, 17, 4), (4, 17, 5), (2, 19, 1)])
+def test_pack_attention_smoke_query_matches_run_attention_smoke(oracle, heads, rows, parts):
+    """main.rs:1334-1362: tile = head + heads * partition; a slice holds the
+    partition's balanced row range (balanced_range) of that head, row-major
+    with the width padded from 72 to 80, padding 0."""
+    width, padded = 72, 80
+    x = (np.arange(heads * rows * width, dtype=np.uint32) % 65000 + 1).astype(np.uint16)
+    got = oracle.pack_tiled(x, [heads, rows, width], 0, 0, heads * parts, 1,
+                            _attention_output(heads, parts))
+    x3 = x.reshape(heads, rows, width)
+    offset = 0
+    for tile in range(heads * parts):
+        head, partition = tile % heads, tile // heads
+        row_start, count = _balanced_range(rows, parts, partition)
+        for linear in range(count * padded):
+            local_row, column = divmod(linear, padded)
+            want = x3[head, row_start + local_row, column] if column < width else 0
+            assert got[offset + linear] == want
+        offset += count * padded
+    assert got.size == offset
+
+
+def test_pack_transposed_orders_place_every_element_once(oracle):
+    """AMP TransposedRight / TransposedLeft / Output / TransposedOutput and
+    transposed block-major shards: every logical element lands once and the
+    padding is zero (bijection of storage.rs's maps over the shard)."""
+    shape = [2, 32, 48]
+    x = (np.arange(np.prod(shape), dtype=np.uint32) + 1).astype(np.uint16)
+    axes = [dict(axis=("end", 3), partitions=2, block_size=1)]
+    for kind, variant, rb, cb in [(1, oracle.AMP_TRANSPOSED_RIGHT, 0, 0),
+                                  (1, oracle.AMP_TRANSPOSED_LEFT, 0, 0),
+                                  (1, oracle.AMP_OUTPUT, 0, 0),
+                                  (1, oracle.AMP_TRANSPOSED_OUTPUT, 0, 0),
+                                  (2, 1, 16, 16), (2, 0, 32, 16)]:
+        got = oracle.pack_tiled(x, shape, kind, variant, 2, 1, axes, rb, cb)
+        assert sorted(got.tolist()) == sorted(x.tolist()), (kind, variant)
