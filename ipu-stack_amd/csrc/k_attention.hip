@@ -197,6 +197,12 @@ __device__ __forceinline__ void attention_block(
   float m_run = -INFINITY;  // reference point, log2 units (scaled)
   float l_run = 0.0f;       // this lane's share of the row sum
   half8_t pp[2][2];         // fp16 probabilities of the last softmax
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pp[st][h][e] = (half_t)0.0f;  // "block -1"
   const uint32_t qi = wq0 + lane % 32;
 
   // Fragment reads.  K fragment (first operand of S^T = K Q^T): lane holds
@@ -384,31 +390,30 @@ __device__ __forceinline__ void attention_block(
     kb_step = kbase;
     vb_step = vbase;
     asm volatile("" : "+v"(kb_step), "+v"(vb_step));
+    // One path for every step (separate paths for the first block and for
+    // blocks past this wave's last made the compiler copy the output
+    // accumulators between register sets): the first step's output MFMAs
+    // add the zero probabilities pp starts with, and past the wave's last
+    // block every key is masked, so the softmax yields zeros and only the
+    // pending output update of the wave's last block counts.
     float16_t s[2];
-    if (kbi > 0 && kbi < nproc) {
-      cluster.template operator()<true>(s, lk, lv, nk, nv, kbi);
-      softmax(s, kbi);
-    } else if (kbi == 0) {
-      cluster.template operator()<false>(s, lk, lv, nk, nv, kbi);
-      softmax(s, kbi);
-    } else {
-      // Past this wave's last block: the DMA, and the pending output update.
-      const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
-#pragma unroll
-      for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, nk, next * k_block_bytes);
-#pragma unroll
-      for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_v(i, nv, kbi * v_block_bytes);
-      if (kbi == nproc) pv_only(lv);
-    }
+    cluster.template operator()<true>(s, lk, lv, nk, nv, kbi);
+    softmax(s, kbi);
   };
 
   // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j).
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, lds_k0, 0);
-  for (uint32_t kbi = 0; kbi < nblocks; kbi += 2) {
+  // Both steps of a pair run unconditionally, so the loop body is one
+  // straight path (a skipped second step made the compiler merge the output
+  // accumulators from two paths with register copies); an odd last block
+  // runs after the loop.
+  uint32_t kbi = 0;
+  for (; kbi + 1 < nblocks; kbi += 2) {
     step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
-    if (kbi + 1 < nblocks) step(lds_k1, lds_v0, lds_k0, lds_v1, kbi + 1);
+    step(lds_k1, lds_v0, lds_k0, lds_v1, kbi + 1);
   }
+  if (kbi < nblocks) step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
   // V of the last block (and every DMA) has landed after this barrier.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
