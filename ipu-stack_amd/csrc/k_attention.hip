@@ -30,11 +30,14 @@
 //     registers, and the matching V^T fragments come from the row-major V
 //     tile through ds_read_b64_tr_b16, whose 4-key runs are chosen to follow
 //     the score accumulator's key order;
-//   * the running max moves only when a block's max exceeds it by more than
-//     kRescaleSlack (log2 units): the result is exact for any reference
-//     point, probabilities stay <= 2^kRescaleSlack, and most blocks skip the
-//     rescale of the output accumulators and the exchange of the max with
-//     the partner lane;
+//   * the reference point (running max) moves only when some probability of
+//     a block would exceed 2^kRescaleSlack, which the block's probability
+//     sum bounds, so no max over the scores is taken on the common path:
+//     the result is exact for any reference point, and most blocks skip the
+//     max, the rescale of the output accumulators and the exchange with the
+//     partner lane;
+//   * K and V fragment offsets are computed once per lane (XOR swizzles of
+//     one base), so the cluster's LDS reads take immediate offsets only;
 //   * causal: key blocks past the workgroup's last query are never loaded, a
 //     wave skips blocks past its own last query.
 //   * causal: one workgroup runs query blocks n - 1 - i and then i of one
@@ -56,6 +59,7 @@ constexpr int kQueriesPerBlock = 128;
 constexpr int kKeysPerBlock = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
+constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, dword 3 of the descriptor
 
 typedef short short4_t __attribute__((vector_size(8)));
@@ -215,8 +219,8 @@ __device__ __forceinline__ void attention_block(
   // columns d0 + 4 (s % 4) .. +3).  Offsets are those of the first rows
   // XORed with the k step (chunk 2 ks: bits 5..) or d tile (chunk 4 dt: bits
   // 6..), since both swizzles XOR the chunk with row bits; other rows add a
-  // constant.  kb_step / vb_step are reloaded opaquely each step so the XORs
-  // stay in the loop instead of taking one register per offset.
+  // constant (an immediate offset of the LDS read).  The per-k-step and
+  // per-d-tile offsets are computed once and stay in registers.
   const uint32_t kbase = k_off<D>(lane % 32, lane / 32);
   uint32_t vbase;
   {
@@ -224,13 +228,17 @@ __device__ __forceinline__ void attention_block(
     const uint32_t d = 16 * dg + 4 * (sl % 4);
     vbase = v_off<D>(4 * g + sl / 4, d / 8) + (d % 8) * 2;
   }
-  uint32_t kb_step = kbase, vb_step = vbase;
+  uint32_t kofs[kKS], vofs[kDT];
+#pragma unroll
+  for (uint32_t ks = 0; ks < kKS; ++ks) kofs[ks] = kbase ^ (ks << 5);
+#pragma unroll
+  for (uint32_t dt = 0; dt < kDT; ++dt) vofs[dt] = vbase ^ (dt << 6);
   auto kfrag = [&](const uint8_t* lk, uint32_t st, uint32_t ks) __attribute__((always_inline)) {
-    const uint8_t* p = lk + (kb_step ^ (ks << 5)) + st * 32 * KvTile<D>::kRowBytes;
+    const uint8_t* p = lk + kofs[ks] + st * 32 * KvTile<D>::kRowBytes;
     return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(p));
   };
   auto vfrag = [&](const uint8_t* lv, uint32_t st, uint32_t h, uint32_t dt) __attribute__((always_inline)) {
-    const uint8_t* p = lv + (vb_step ^ (dt << 6)) + (32 * st + 16 * h) * KvTile<D>::kRowBytes;
+    const uint8_t* p = lv + vofs[dt] + (32 * st + 16 * h) * KvTile<D>::kRowBytes;
     const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
     const short4_t hi =
         __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 8 * KvTile<D>::kRowBytes));
@@ -264,17 +272,22 @@ __device__ __forceinline__ void attention_block(
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
-    // K fragments two k steps ahead, V fragments one.
+    // K and V fragments two k steps ahead (four MFMAs between a fragment's
+    // read and its use, which covers the LDS latency).
     constexpr uint32_t kAhead = 2;
-    half8_t kf[kAhead][2], vf[2];
+    half8_t kf[kAhead][2], vf[kAhead][2];
+    // PV MFMA n = 2 ks + st of 16: (st, h) pair n / kDT, d tile n % kDT.
+    auto pv_frag = [&](uint32_t ks, uint32_t st) __attribute__((always_inline)) {
+      const uint32_t n = 2 * ks + st, c = n / kDT, dt = n % kDT;
+      return vfrag(lv, c / 2, c % 2, dt);
+    };
 #pragma unroll
     for (uint32_t ks = 0; ks < kAhead; ++ks)
 #pragma unroll
-      for (int st = 0; st < 2; ++st) kf[ks][st] = kfrag(lk, st, ks);
-    if constexpr (WithPv) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) vf[st] = vfrag(lv, 0, 0, st);
-    }
+      for (int st = 0; st < 2; ++st) {
+        kf[ks][st] = kfrag(lk, st, ks);
+        if constexpr (WithPv) vf[ks][st] = pv_frag(ks, st);
+      }
     __builtin_amdgcn_sched_barrier(0);
     // Raised priority while this wave feeds the matrix pipe: the other wave
     // on the SIMD fills the gaps with its softmax.
@@ -285,22 +298,16 @@ __device__ __forceinline__ void attention_block(
       for (int st = 0; st < 2; ++st) {
         s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks % kAhead][st], qf[ks], s[st], 0, 0, 0);
         if constexpr (WithPv) {
-          // PV MFMA n = 2 ks + st of 16: (st, h) pair n / kDT, d tile n % kDT.
           const uint32_t n = 2 * ks + st, c = n / kDT, dt = n % kDT;
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[st], pp[c / 2][c % 2], o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[ks % kAhead][st], pp[c / 2][c % 2], o[dt],
+                                                         0, 0, 0);
         }
       }
       if (ks + kAhead < kKS) {
 #pragma unroll
-        for (int st = 0; st < 2; ++st) kf[ks % kAhead][st] = kfrag(lk, st, ks + kAhead);
-      }
-      if constexpr (WithPv) {
-        if (ks + 1 < kKS) {
-#pragma unroll
-          for (int st = 0; st < 2; ++st) {
-            const uint32_t n = 2 * (ks + 1) + st, c = n / kDT, dt = n % kDT;
-            vf[st] = vfrag(lv, c / 2, c % 2, dt);
-          }
+        for (int st = 0; st < 2; ++st) {
+          kf[ks % kAhead][st] = kfrag(lk, st, ks + kAhead);
+          if constexpr (WithPv) vf[ks % kAhead][st] = pv_frag(ks + kAhead, st);
         }
       }
       // DMA instructions spread over the k steps: K tile first, then V.
@@ -331,27 +338,68 @@ __device__ __forceinline__ void attention_block(
     const uint32_t kb = kbi * kKeysPerBlock;
     const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
     if (need_mask) {
+      // Key kb + 4 (lane / 32) + x is allowed iff x <= lim (the last allowed
+      // key is min(qi, key_rows - 1) causal, key_rows - 1 otherwise; key_rows
+      // < 2^30, so lim fits an int).
+      const uint32_t last = Causal && qi < key_rows - 1 ? qi : key_rows - 1;
+      const int lim = (int)last - (int)(kb + 4 * (lane / 32));
+      // One compare into VCC and one select per score (compares into SGPR
+      // pairs, as the compiler hoists them, run out of SGPRs).  The scores
+      // come straight from MFMAs, and the hazard padding the compiler gives
+      // its own VALU reads of MFMA results does not cover inline assembly:
+      // 24 wait states first.
+      const float ninf = -INFINITY;
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t kj = kb + 32 * st + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-          if ((Causal && kj > qi) || kj >= key_rows) s[st][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          asm volatile("v_cmp_gt_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %0, %3, vcc"
+                       : "+v"(s[st][r])
+                       : "n"(32 * st + 8 * (r / 4) + r % 4), "v"(lim), "v"(ninf)
+                       : "vcc");
     }
-    // Max over this lane's 32 keys.  The partner lane (lane ^ 32: the other
-    // 32 keys of the same query) is consulted only when some lane's max
-    // passes the slack, so both halves always share one reference point;
-    // the max is finite (at least one allowed key per query).
-    float mx = s[0][0];
+    // Probabilities against the current reference point, and this lane's
+    // share of the block's row sum.  The row sum adds the fp16
+    // probabilities that the MFMA consumes: pairs, then quads, in fp16
+    // (each p <= 2^kRescaleSlack on the accepted path, so a quad sum stays
+    // far inside the fp16 range and carries at most two roundings), then
+    // fp32 accumulation with v_dot2.
+    auto exps = [&](float neg_m, half8_t (*pf)[2]) __attribute__((always_inline)) {
+      float sum = 0.0f;
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+      for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-    mx *= scale_log2;
-    if (__any(mx > m_run + kRescaleSlack)) {
-      mx = max_with_partner(mx);
-      const float m_new = mx > m_run + kRescaleSlack ? mx : m_run;
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            pf[st][h][e] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
+          const half2_t s01 = half2_t{pf[st][h][0], pf[st][h][1]} + half2_t{pf[st][h][2], pf[st][h][3]};
+          const half2_t s45 = half2_t{pf[st][h][4], pf[st][h][5]} + half2_t{pf[st][h][6], pf[st][h][7]};
+          sum = __builtin_amdgcn_fdot2(s01 + s45, half2_t{1, 1}, sum, false);
+        }
+      return sum;
+    };
+    // The reference point moves only when some probability would exceed
+    // 2^kRescaleSlack, found without a max over the scores: every p is at
+    // most the lane's block sum, so a block sum <= 2^kRescaleSlack accepts
+    // the block (overflow to inf and NaN, as against the -inf start, fail
+    // the test).  Otherwise the max of the query's 64 keys (this lane and
+    // its partner lane ^ 32, so both halves share one reference point; it is
+    // finite, as every processed block holds an allowed key per query)
+    // becomes the reference point, the output and sum are rescaled, and the
+    // probabilities are recomputed (all <= 1).  Exact for any reference
+    // point.
+    half8_t pf[2][2];
+    float sum = exps(-m_run, pf);
+    if (__any(!(sum <= kSumLimit))) {
+      float mx = s[0][0];
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
+      mx = max_with_partner(mx * scale_log2);
+      const float m_new = mx > m_run ? mx : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
@@ -359,25 +407,13 @@ __device__ __forceinline__ void attention_block(
       for (uint32_t dt = 0; dt < kDT; ++dt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      sum = exps(-m_run, pf);
     }
-    const float neg_m = -m_run;
+    l_run += sum;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8_t pf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          pf[e] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
-        // The row sum adds the fp16 probabilities that the MFMA consumes:
-        // pairs, then quads, in fp16 (each p <= 2^kRescaleSlack, so a quad
-        // sum stays far inside the fp16 range and carries at most two
-        // roundings), then fp32 accumulation with v_dot2.
-        const half2_t s01 = half2_t{pf[0], pf[1]} + half2_t{pf[2], pf[3]};
-        const half2_t s45 = half2_t{pf[4], pf[5]} + half2_t{pf[6], pf[7]};
-        l_run = __builtin_amdgcn_fdot2(s01 + s45, half2_t{1, 1}, l_run, false);
-        pp[st][h] = pf;
-      }
+      for (int h = 0; h < 2; ++h) pp[st][h] = pf[st][h];
   };
 
   auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi)
@@ -387,9 +423,6 @@ __device__ __forceinline__ void attention_block(
     // step overwrites.  The last block re-fetches its K tile: the DMA stays
     // unconditional, which keeps the compiler's wait counting exact.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    kb_step = kbase;
-    vb_step = vbase;
-    asm volatile("" : "+v"(kb_step), "+v"(vb_step));
     // One path for every step (separate paths for the first block and for
     // blocks past this wave's last made the compiler copy the output
     // accumulators between register sets): the first step's output MFMAs
@@ -401,9 +434,15 @@ __device__ __forceinline__ void attention_block(
     softmax(s, kbi);
   };
 
-  // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j).
+  // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j).  The first
+  // step's output MFMAs multiply zero probabilities with V stage 1, which
+  // is zeroed here (whatever an earlier kernel left in LDS may hold
+  // non-finite fp16 patterns; 0 * inf is NaN).
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, lds_k0, 0);
+#pragma unroll
+  for (uint32_t i = 0; i < kTile / 16 / kThreads; ++i)
+    *reinterpret_cast<u32x4*>(lds_v1 + (i * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
   // Both steps of a pair run unconditionally, so the loop body is one
   // straight path (a skipped second step made the compiler merge the output
   // accumulators from two paths with register copies); an odd last block

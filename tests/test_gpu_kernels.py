@@ -386,6 +386,50 @@ def test_attention_reference_smoke_tolerance(ipus, oracle, ctx):
     assert err.max() <= 0.012 and np.sqrt(np.mean(err ** 2)) <= 0.003
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("streams,s,d,amp", [(2, 512, 128, 8.0), (2, 384, 64, 12.0),
+                                            (1, 300, 96, 4.0)])
+def test_attention_moving_reference_point(ipus, oracle, ctx, causal, streams, s, d, amp):
+    """Scores that keep rising along the keys (large queries, keys with a
+    rising offset) move the kernel's reference point in many blocks, so the
+    rescale path (max, partner exchange, output and sum rescale, recomputed
+    probabilities) runs often and between blocks that skip it."""
+    rng = np.random.default_rng(int(amp) * 131 + d)
+    q = (rng.standard_normal((streams, s, d)) * amp).astype(np.float16)
+    ramp = np.linspace(0.0, 3.0, s, dtype=np.float32)[None, :, None]
+    k = (rng.standard_normal((streams, s, d)).astype(np.float32) + ramp).astype(np.float16)
+    v = rng.standard_normal((streams, s, d)).astype(np.float16)
+    q, k, v = (x.view(np.uint16).ravel() for x in (q, k, v))
+    got = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * d * 4, [q, k, v],
+              [streams, s, s, d, d, 0, int(causal), 0], np.float32).reshape(-1, d)
+    want = oracle.attention(oracle.f16_to_f32(q), oracle.f16_to_f32(k), oracle.f16_to_f32(v),
+                            streams, s, s, d, d, causal, None)
+    assert np.isfinite(got).all()
+    assert fp16_close(got, want, FP16_TOL)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_after_nan_filled_lds(ipus, oracle, ctx, d):
+    """A GEMM over all-NaN operands first leaves NaN patterns in the LDS of
+    every CU; the attention that follows must not pick any of them up (its
+    first step multiplies zero probabilities with a V stage that no DMA has
+    filled yet, which the kernel zeroes)."""
+    n = 4096
+    nan = np.full(n * 256, 0xFFFF, np.uint16)
+    run(ctx, "ipu_stack_gemm_f16", n * n * 2, [nan, nan[: 256 * n]], [1, n, n, 256, 0, 0, 0, 0])
+    streams, s = 4, 512
+    q = synth(ipus, streams * s * d, 71, 1, 1)
+    k = synth(ipus, streams * s * d, 71, 2, 1)
+    v = synth(ipus, streams * s * d, 71, 3, 1)
+    for causal in (True, False):
+        got = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * d * 4, [q, k, v],
+                  [streams, s, s, d, d, 0, int(causal), 0], np.float32).reshape(-1, d)
+        want = oracle.attention(oracle.f16_to_f32(q), oracle.f16_to_f32(k), oracle.f16_to_f32(v),
+                                streams, s, s, d, d, causal, None)
+        assert np.isfinite(got).all()
+        assert fp16_close(got, want, FP16_TOL)
+
+
 def test_attention_uniform_values_give_values(ipus, oracle, ctx):
     """Invariant: V rows all equal -> O = that row for every query (softmax rows sum to 1)."""
     streams, s, d = 2, 256, 128
