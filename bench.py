@@ -23,8 +23,9 @@ JSON line on stdout.
 Other modes turn rocprofv3 output of a bench run into the committed
 summaries under profiles/ through the package's own rocprof ingestion
 (ipu-stack_amd/profiling.py): --summarize-trace (kernel durations per kernel,
-warmup launches excluded) and --summarize-traffic (HBM bytes per launch from
-FETCH_SIZE / WRITE_SIZE, scaled by the plain copy kernel's counters).
+warmup launches excluded), --summarize-traffic (HBM bytes per launch from
+FETCH_SIZE / WRITE_SIZE, scaled by the plain copy kernel's counters) and
+--summarize-counters (shader clock and MFMA-pipe utilisation per kernel).
 """
 from __future__ import annotations
 
@@ -492,6 +493,50 @@ def summarize_traffic(fetch_dir: str, write_dir: str, kernel: str, copy_kernel: 
     }
 
 
+def summarize_counters(directory: str, skip: int, command: str, xcds: int = 8,
+                       simds: int = 1024) -> str:
+    """MFMA-pipe utilisation and shader clock per kernel from one rocprofv3
+    --pmc pass holding SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE (and any
+    other counters, reported as medians).  GRBM_GUI_ACTIVE is summed over the
+    XCDs, so the shader clock is GRBM_GUI_ACTIVE / xcds / duration;
+    SQ_VALU_MFMA_BUSY_CYCLES counts 32 cycles per v_mfma_f32_32x32x16_f16
+    over all SIMDs, so the utilisation is that over shader cycles x SIMDs."""
+    prof = _profiling()
+    report = prof.from_rocprof(counter_csv=directory)
+    keep = _timed_phases(report, skip)
+    rows = {}
+    for tile in report.tiles:
+        for smp in tile.samples:
+            if smp.step.phase not in keep:
+                continue
+            md = {m.name[len(prof.COUNTER_PREFIX):]: float(m.value) for m in smp.step.metadata
+                  if m.name.startswith(prof.COUNTER_PREFIX)}
+            md["ns"] = float((smp.end_cycle - smp.start_cycle) % (1 << 32))
+            rows.setdefault(smp.step.kernel, []).append(md)
+    names = sorted({c for v in rows.values() for r in v for c in r} - {"ns"})
+    lines = ["Command (from the repository root, `export TMPDIR=/tmp`):", "", f"    {command}", "",
+             f"Summary: `python bench.py --summarize-counters <pmc dir> --skip {skip}` "
+             f"(ipu-stack_amd/profiling.py: rocprofv3 counter collection -> ProfileReport); "
+             f"medians over each kernel's dispatches after its first {skip}.  Shader clock = "
+             f"GRBM_GUI_ACTIVE / {xcds} XCDs / duration; MFMA-pipe utilisation = "
+             f"SQ_VALU_MFMA_BUSY_CYCLES / (shader cycles x {simds} SIMDs).", "",
+             "| kernel | dispatches | median ns | " + " | ".join(names) +
+             " | shader clock | MFMA-pipe utilisation |",
+             "|---|---|---|" + "---|" * len(names) + "---|---|"]
+    for kernel, v in sorted(rows.items()):
+        med = {c: float(np.median([r[c] for r in v if c in r])) for c in names + ["ns"]
+               if any(c in r for r in v)}
+        ns = med["ns"]
+        cycles = med.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+        clock = f"{cycles / ns:.2f} GHz" if cycles and ns else "-"
+        busy = med.get("SQ_VALU_MFMA_BUSY_CYCLES")
+        util = f"{busy / (cycles * simds):.0%}" if busy is not None and cycles else "-"
+        cells = [f"{med[c]:.4g}" if c in med else "-" for c in names]
+        lines.append(f"| `{kernel}` | {len(v)} | {ns:.0f} | " + " | ".join(cells) +
+                     f" | {clock} | {util} |")
+    return "\n".join(lines) + "\n"
+
+
 def device_name(info: dict) -> str:
     """The HIP device name; where the runtime leaves it empty, the product
     name the amdgpu driver exposes in sysfs."""
@@ -576,11 +621,16 @@ def main() -> int:
                     help="markdown summary of a rocprofv3 --kernel-trace output directory")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="JSON traffic summary of two rocprofv3 --pmc runs of --traffic-probe")
+    ap.add_argument("--summarize-counters", metavar="DIR",
+                    help="markdown MFMA-utilisation / clock summary of a rocprofv3 --pmc pass")
     ap.add_argument("--skip", type=int, default=5, help="warmup dispatches per kernel to drop")
     ap.add_argument("--command", default="", help="command line recorded in a summary")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.skip, args.command), end="")
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.skip, args.command), end="")
         return 0
     if args.summarize_traffic:
         n = 8192
