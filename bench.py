@@ -184,6 +184,29 @@ def bench_memory_chain(ipus, ctx, steps, warmup, n=8192, sets=3):
     return out
 
 
+def bench_amp_layouts(ipus, ctx, steps, warmup, n=8192, sets=3):
+    """The reference's AMP storage conversions on X[8192, 8192] fp16:
+    row-major -> AMP-Left and -> AMP-TransposedRight (rearrange_amp_left_f16,
+    rearrange_transposed_right_f16), and unpack of AMP-Output and
+    AMP-TransposedLeft back to row-major (unpack_amp_f16)."""
+    x = [ctx.upload(ipus.synth_f16(n * n, 79, 20 + s, ipus.NORMAL)) for s in range(sets)]
+    y = [ctx.alloc(n * n * 2) for _ in range(sets)]
+    out = {}
+    for name, order in (("rearrange_amp_left", 0), ("rearrange_amp_transposed_right", 1)):
+        out[name] = timed(
+            ctx, lambda i, o=order: ctx.launch("ipu_stack_rearrange_row_major_f16", y[i % sets],
+                                               [x[i % sets]], [n, n, o, n, n, 32, 16, 1]),
+            steps, warmup)
+    for name, source in (("unpack_amp_output", 0), ("unpack_amp_transposed_left", 1)):
+        out[name] = timed(
+            ctx, lambda i, src=source: ctx.launch("ipu_stack_unpack_amp_f16", y[i % sets],
+                                                  [x[i % sets]], [1, n, n, n, n, src]),
+            steps, warmup)
+    for b in x + y:
+        b.free()
+    return out
+
+
 def bench_gelu(ipus, ctx, steps, warmup, rows=4096, cols=16384, sets=3):
     n = rows * cols
     x = [ctx.upload(ipus.synth_f16(n, 88, s, ipus.NORMAL)) for s in range(sets)]
@@ -554,7 +577,8 @@ def device_name(info: dict) -> str:
 
 
 LEGS = ("mfma_calibration", "gemm_f32_4096", "gemm_f16_256", "attention_causal_s4096",
-        "attention_noncausal_s2048", "memory_chain", "gelu_4096x16384", "mlp_graph")
+        "attention_noncausal_s2048", "memory_chain", "amp_layouts", "gelu_4096x16384",
+        "mlp_graph")
 
 
 def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
@@ -593,6 +617,10 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
                     "reduce_rows": n * n * 2 + n * 4, "reduce_rows_row_major": n * n * 2 + n * 4}
         for k, t in chain.items():
             results[k] = leg_entry(t, bytes_rw[k], "gbps", PEAK_HBM_GBPS)
+            log(f"{k}: {results[k]}")
+    if want("amp_layouts"):
+        for k, t in bench_amp_layouts(ipus, ctx, args.steps, 3).items():
+            results[k] = leg_entry(t, 2 * n * n * 2, "gbps", PEAK_HBM_GBPS)
             log(f"{k}: {results[k]}")
     if want("gelu_4096x16384"):
         t = bench_gelu(ipus, ctx, args.steps, 3)

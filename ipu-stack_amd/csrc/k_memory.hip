@@ -231,6 +231,92 @@ __global__ __launch_bounds__(kThreads) void unpack_f16_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// AMP orders, unpadded and 16-byte aligned: 16-byte chunks instead of
+// elements.  AMP-Left and AMP-TransposedRight keep every run of 8 columns
+// (8-aligned) contiguous (panels of 16 columns, 16 x 16 blocks stored row by
+// row), so a chunk of a row-major row is a chunk of the stored tensor.  A
+// workgroup takes a tile 64 columns wide: each row-major row of the tile is
+// one 128-byte line, and the stored side of the tile is 4 panels of 64 rows
+// x 32 bytes (AMP-Left) or 2 x 4 blocks of 512 bytes (TransposedRight), so
+// both sides are read and written in runs of 256 bytes or more per wave.
+// ToRowMajor runs the same map the other way (stored -> row-major).
+// AMP-Left folds matrices into the rows (storage.rs:250-266), so `rows` is
+// all matrices' rows and blockIdx.y is 0; TransposedRight is per matrix.
+// ---------------------------------------------------------------------------
+template <uint32_t Order, bool ToRowMajor>
+__global__ __launch_bounds__(kThreads) void amp_tile_f16_kernel(uint16_t* __restrict__ dst,
+                                                                const uint16_t* __restrict__ src,
+                                                                uint32_t rows, uint32_t columns,
+                                                                uint32_t tiles_c) {
+  constexpr uint32_t kTileRows = Order == kOrderAmpLeft ? 64 : 32;
+  constexpr uint32_t kPer = kTileRows * 8 / kThreads;  // chunks per thread
+  const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  const uint64_t me = (uint64_t)rows * columns;
+  src += blockIdx.y * me;
+  dst += blockIdx.y * me;
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i) {
+    const uint32_t k = threadIdx.x + kThreads * i;
+    const uint32_t r = tr * kTileRows + k / 8, c = tc * 64 + (k % 8) * 8;
+    if (r >= rows || c >= columns) continue;
+    const uint64_t row_major = (uint64_t)r * columns + c;
+    const uint64_t stored = Order == kOrderAmpLeft
+                                ? amp_left_index(rows, r, c)
+                                : amp_transposed_right_index(rows, columns, r, c);
+    if constexpr (ToRowMajor)
+      store16_nt(dst + row_major, load16_nt(src + stored));
+    else
+      store16_nt(dst + stored, load16_nt(src + row_major));
+  }
+}
+
+// Unpack AMP-Output (pair-permuted 16-column micros, storage.rs:329-340),
+// unpadded and aligned: a thread moves one micro (32 bytes), restoring the
+// pair order in registers: logical pair p sits at physical pair
+// (p % 4) * 2 + p / 4.  A workgroup takes 64 rows x 64 columns: four
+// threads cover a 128-byte row line, and a wave reads 512-byte runs (16
+// rows) of each of the tile's four panels.
+__global__ __launch_bounds__(kThreads) void unpack_amp_output_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows,
+    uint32_t columns, uint32_t tiles_c) {
+  const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  const uint32_t r = tr * 64 + threadIdx.x / 4, c = tc * 64 + (threadIdx.x % 4) * kMicro;
+  if (r >= rows || c >= columns) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint16_t* s = src + blockIdx.y * me + amp_output_index(rows, r, c);
+  const u32x4 a = load16_nt(s), b = load16_nt(s + 8);
+  // word = one pair; logical pairs 0-3 <- physical 0, 2, 4, 6, pairs 4-7 <- 1, 3, 5, 7
+  const u32x4 lo = {a[0], a[2], b[0], b[2]}, hi = {a[1], a[3], b[1], b[3]};
+  uint16_t* d = dst + blockIdx.y * me + (uint64_t)r * columns + c;
+  store16_nt(d, lo);
+  store16_nt(d + 8, hi);
+}
+
+// Unpack AMP-TransposedLeft (AMP-Left of the transpose, storage.rs:326-328),
+// unpadded and aligned: the 16 rows of panel q are stored [columns][16], a
+// transposed strip.  A thread loads 8 columns x 8 rows of it (one half of
+// each column's 16 rows), transposes the 8 x 8 block in registers and writes
+// 8 row segments of 16 bytes; lanes pair up on the two halves, so a wave
+// reads 8 KiB of one strip and writes 512-byte runs of 16 rows.
+__global__ __launch_bounds__(kThreads) void unpack_amp_transposed_left_f16_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows,
+    uint32_t columns, uint32_t col_groups) {
+  const uint32_t panel = blockIdx.x / col_groups, group = blockIdx.x % col_groups;
+  const uint32_t half = threadIdx.x % 2;
+  const uint32_t c0 = (group * (kThreads / 2) + threadIdx.x / 2) * 8;
+  if (c0 >= columns) return;
+  const uint64_t me = (uint64_t)rows * columns;
+  const uint16_t* s = src + blockIdx.y * me + (uint64_t)panel * columns * kMicro + half * 8;
+  uint16_t* d = dst + blockIdx.y * me + (uint64_t)(panel * kMicro + half * 8) * columns + c0;
+  u32x4 in[8], out[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) in[i] = load16_nt(s + (uint64_t)(c0 + i) * kMicro);
+  transpose8x8_u16(in, out);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) store16_nt(d + (uint64_t)j * columns, out[j]);
+}
+
+// ---------------------------------------------------------------------------
 // Row sums of a row-major [rows, columns] fp16 matrix, fp32 accumulation.
 // One block per row; 16-byte loads; wave shuffles then LDS across waves.
 // ---------------------------------------------------------------------------
@@ -678,6 +764,30 @@ int launch_transpose_f16(hipStream_t stream, void* dst, const void* src, uint32_
   return hip_status(hipGetLastError());
 }
 
+// The chunked AMP-Left / AMP-TransposedRight kernels for an unpadded,
+// aligned tensor (columns a multiple of 16, and rows too for
+// TransposedRight, as the orders require); false when the grid does not fit.
+template <bool ToRowMajor>
+bool launch_amp_tile(hipStream_t stream, void* dst, const void* src, uint32_t order,
+                     uint32_t matrices, uint32_t rows, uint32_t columns) {
+  const uint32_t tiles_c = ceil_div(columns, 64);
+  if (order == kOrderAmpLeft) {
+    const uint64_t flat = (uint64_t)matrices * rows;
+    const uint64_t tiles = ceil_div(flat, 64) * (uint64_t)tiles_c;
+    if (flat > 0xffffffffull || tiles > 0x7fffffffull) return false;
+    hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpLeft, ToRowMajor>), dim3((uint32_t)tiles),
+                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
+                       (uint32_t)flat, columns, tiles_c);
+    return true;
+  }
+  const uint64_t tiles = (uint64_t)ceil_div(rows, 32) * tiles_c;
+  if (tiles > 0x7fffffffull || matrices > 65535) return false;
+  hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpTransposedRight, ToRowMajor>),
+                     dim3((uint32_t)tiles, matrices), dim3(kThreads), 0, stream, (uint16_t*)dst,
+                     (const uint16_t*)src, rows, columns, tiles_c);
+  return true;
+}
+
 int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_t target_order,
                          uint32_t row_block, uint32_t column_block, uint32_t matrices,
                          uint32_t logical_rows, uint32_t physical_rows, uint32_t logical_columns,
@@ -712,6 +822,10 @@ int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_
     hipLaunchKernelGGL(block_major_f16_kernel, dim3(tiles_r * tiles_c, matrices), dim3(kThreads), 0,
                        stream, (uint16_t*)dst, (const uint16_t*)src, physical_rows,
                        physical_columns, row_block, column_block, tiles_c);
+  } else if (target_order != kOrderBlockMajor && logical_rows == physical_rows &&
+             logical_columns == physical_columns && aligned16(dst) && aligned16(src) &&
+             launch_amp_tile<false>(stream, dst, src, target_order, matrices, physical_rows,
+                                    physical_columns)) {
   } else {
     hipLaunchKernelGGL(rearrange_f16_general_kernel, dim3(ceil_div(total, kThreads)),
                        dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
@@ -735,9 +849,29 @@ int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t s
   if (physical_columns % 2 != 0) return IPUS_ERROR_INVALID_ARGUMENT;
   const uint64_t total = (uint64_t)matrices * physical_rows * physical_columns;
   if (total == 0) return 0;
-  hipLaunchKernelGGL(unpack_f16_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads), 0, stream,
-                     (uint16_t*)dst, (const uint16_t*)src, source_order, logical_rows,
-                     physical_rows, logical_columns, physical_columns, total);
+  const bool unpadded = logical_rows == physical_rows && logical_columns == physical_columns &&
+                        aligned16(dst) && aligned16(src);
+  const uint64_t out_tiles = (uint64_t)ceil_div(physical_rows, 64) * ceil_div(physical_columns, 64);
+  if (unpadded && source_order == kUnpackAmpOutput && out_tiles <= 0x7fffffffull &&
+      matrices <= 65535) {
+    const uint32_t tiles_c = ceil_div(physical_columns, 64);
+    hipLaunchKernelGGL(unpack_amp_output_f16_kernel, dim3((uint32_t)out_tiles, matrices),
+                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
+                       physical_rows, physical_columns, tiles_c);
+  } else if (unpadded && source_order == kUnpackAmpTransposedLeft && physical_columns % 8 == 0 &&
+             matrices <= 65535 &&
+             (uint64_t)(physical_rows / kMicro) * ceil_div(physical_columns, 8 * (kThreads / 2)) <=
+                 0x7fffffffull) {
+    const uint32_t col_groups = ceil_div(physical_columns, 8 * (kThreads / 2));
+    hipLaunchKernelGGL(unpack_amp_transposed_left_f16_kernel,
+                       dim3(physical_rows / kMicro * col_groups, matrices), dim3(kThreads), 0,
+                       stream, (uint16_t*)dst, (const uint16_t*)src, physical_rows,
+                       physical_columns, col_groups);
+  } else {
+    hipLaunchKernelGGL(unpack_f16_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads), 0,
+                       stream, (uint16_t*)dst, (const uint16_t*)src, source_order, logical_rows,
+                       physical_rows, logical_columns, physical_columns, total);
+  }
   return hip_status(hipGetLastError());
 }
 
@@ -894,6 +1028,8 @@ int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint
     hipLaunchKernelGGL(block_major_to_row_major_f16_kernel, dim3(tiles_r * tiles_c, matrices),
                        dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src, rows,
                        columns, row_block, column_block, tiles_c);
+  } else if (source_order != kOrderBlockMajor && aligned16(dst) && aligned16(src) &&
+             launch_amp_tile<true>(stream, dst, src, source_order, matrices, rows, columns)) {
   } else {
     hipLaunchKernelGGL(to_row_major_f16_general_kernel, dim3(ceil_div(total, kThreads)),
                        dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,

@@ -97,6 +97,35 @@ def test_unpack_bit_exact(ipus, oracle, ctx, source, matrices, lr, pr, lc, pc):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("order", [0, 1])
+@pytest.mark.parametrize("matrices,rows,cols", [
+    (1, 48, 16), (1, 64, 64), (3, 96, 208), (2, 1024, 2048), (1, 4096, 4096)])
+def test_rearrange_amp_unpadded_bit_exact(ipus, oracle, ctx, order, matrices, rows, cols):
+    """The chunked AMP-Left / AMP-TransposedRight path (unpadded, aligned;
+    partial 64-column and row tiles included), both directions."""
+    x = synth(ipus, matrices * rows * cols, 16, 6, 1)
+    got = run(ctx, "ipu_stack_rearrange_row_major_f16", x.nbytes, [x],
+              [rows, rows, order, cols, cols, 32, 16, matrices])
+    want = oracle.rearrange_row_major_f16(x, order, matrices, rows, rows, cols, cols, 32, 16)
+    assert np.array_equal(got, want)
+    back = run(ctx, "ipu_stack_rearrange_to_row_major_f16", x.nbytes, [got],
+               [order, 32, 16, matrices, rows, cols])
+    assert np.array_equal(back, x)
+
+
+@pytest.mark.parametrize("source,matrices,rows,cols", [
+    (0, 1, 16, 16), (0, 3, 96, 208), (0, 2, 1024, 2048), (0, 1, 4096, 4096), (0, 1, 5, 32),
+    (1, 1, 16, 16), (1, 3, 96, 208), (1, 2, 1024, 2048), (1, 1, 4096, 4096), (1, 2, 32, 40),
+    (1, 1, 16, 2056)])
+def test_unpack_unpadded_bit_exact(ipus, oracle, ctx, source, matrices, rows, cols):
+    """The chunked unpack paths: AMP-Output micros with the pair order
+    restored in registers, AMP-TransposedLeft strips by 8 x 8 transposes."""
+    x = synth(ipus, matrices * rows * cols, 17, 7, 1)
+    got = run(ctx, "ipu_stack_unpack_amp_f16", x.nbytes, [x], [matrices, rows, rows, cols, cols, source])
+    want = oracle.unpack_to_row_major_f16(x, source, matrices, rows, rows, cols, cols)
+    assert np.array_equal(got, want)
+
+
 # ---------------------------------------------------------------------------
 # Reductions
 # ---------------------------------------------------------------------------
