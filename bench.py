@@ -516,6 +516,47 @@ def summarize_traffic(fetch_dir: str, write_dir: str, kernel: str, copy_kernel: 
     }
 
 
+def summarize_traffic_table(fetch_dir: str, write_dir: str, skip: int, command: str,
+                            copy_kernel: str = "copy_bytes_kernel",
+                            copy_bytes: int = 8192 * 8192 * 2) -> str:
+    """HBM bytes per dispatch of every kernel of a FETCH_SIZE and a WRITE_SIZE
+    pass (KiB per dispatch, medians after each kernel's first `skip`
+    dispatches), each scaled by the factor that makes `copy_kernel` (which
+    reads and writes `copy_bytes`) read and write exactly its bytes."""
+    prof = _profiling()
+
+    def medians(directory, counter):
+        report = prof.from_rocprof(counter_csv=directory)
+        keep = _timed_phases(report, skip)
+        vals = {}
+        for tile in report.tiles:
+            for smp in tile.samples:
+                if smp.step.phase not in keep:
+                    continue
+                md = {m.name: m.value for m in smp.step.metadata}
+                v = md.get(prof.COUNTER_PREFIX + counter)
+                if v is not None:
+                    vals.setdefault(smp.step.kernel, []).append(float(v))
+        return {k: float(np.median(v)) for k, v in vals.items()}
+
+    fetch, write = medians(fetch_dir, "FETCH_SIZE"), medians(write_dir, "WRITE_SIZE")
+    f_scale = copy_bytes / (fetch[copy_kernel] * 1024.0)
+    w_scale = copy_bytes / (write[copy_kernel] * 1024.0)
+    lines = ["Commands (from the repository root, `export TMPDIR=/tmp`):", ""]
+    lines += [f"    {c}" for c in command.split(" ;; ") if c]
+    lines += ["", f"Summary: `python bench.py --summarize-traffic-table <FETCH_SIZE dir> "
+              f"<WRITE_SIZE dir> --skip {skip}` (ipu-stack_amd/profiling.py's rocprof "
+              f"ingestion); medians over each kernel's dispatches after its first {skip}.  "
+              f"Scales from `{copy_kernel}` ({copy_bytes} bytes read and written): FETCH_SIZE "
+              f"x {f_scale:.3f}, WRITE_SIZE x {w_scale:.3f}.", "",
+              "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read MB | HBM write MB |",
+              "|---|---|---|---|---|"]
+    for k in sorted(set(fetch) & set(write)):
+        lines.append(f"| `{k}` | {fetch[k]:.1f} | {write[k]:.1f} | "
+                     f"{fetch[k] * 1024 * f_scale / 1e6:.2f} | {write[k] * 1024 * w_scale / 1e6:.2f} |")
+    return "\n".join(lines) + "\n"
+
+
 def summarize_counters(directory: str, skip: int, command: str, xcds: int = 8,
                        simds: int = 1024) -> str:
     """MFMA-pipe utilisation and shader clock per kernel from one rocprofv3
@@ -649,6 +690,8 @@ def main() -> int:
                     help="markdown summary of a rocprofv3 --kernel-trace output directory")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="JSON traffic summary of two rocprofv3 --pmc runs of --traffic-probe")
+    ap.add_argument("--summarize-traffic-table", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="markdown HBM bytes per kernel of a FETCH_SIZE and a WRITE_SIZE pass")
     ap.add_argument("--summarize-counters", metavar="DIR",
                     help="markdown MFMA-utilisation / clock summary of a rocprofv3 --pmc pass")
     ap.add_argument("--skip", type=int, default=5, help="warmup dispatches per kernel to drop")
@@ -656,6 +699,11 @@ def main() -> int:
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.skip, args.command), end="")
+        return 0
+    if args.summarize_traffic_table:
+        print(summarize_traffic_table(args.summarize_traffic_table[0],
+                                      args.summarize_traffic_table[1], args.skip, args.command),
+              end="")
         return 0
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.skip, args.command), end="")
