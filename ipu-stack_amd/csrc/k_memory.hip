@@ -830,6 +830,7 @@ int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_
              logical_columns == physical_columns && aligned16(dst) && aligned16(src) &&
              launch_amp_tile<false>(stream, dst, src, target_order, matrices, physical_rows,
                                     physical_columns)) {
+    // launched by launch_amp_tile
   } else {
     hipLaunchKernelGGL(rearrange_f16_general_kernel, dim3(ceil_div(total, kThreads)),
                        dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
@@ -1034,6 +1035,7 @@ int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint
                        columns, row_block, column_block, tiles_c);
   } else if (source_order != kOrderBlockMajor && aligned16(dst) && aligned16(src) &&
              launch_amp_tile<true>(stream, dst, src, source_order, matrices, rows, columns)) {
+    // launched by launch_amp_tile
   } else {
     hipLaunchKernelGGL(to_row_major_f16_general_kernel, dim3(ceil_div(total, kThreads)),
                        dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
