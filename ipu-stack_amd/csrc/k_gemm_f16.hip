@@ -8,34 +8,40 @@
 // Fast kernel (16-byte aligned operands; N and K multiples of 8, and M too
 // when A is transposed; any M, N, K otherwise):
 //   * block tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid, each
-//     wave owns 128 x 128 of C as 4 x 4 tiles of v_mfma_f32_32x32x16_f16;
+//     wave owns 128 x 128 of C as 8 x 8 tiles of v_mfma_f32_16x16x32_f16
+//     (64 accumulators of 4 fp32, in AGPRs); a K step is two 32-k substeps.
+//     On this board the MFMA pipes run under a power limit, and with operands
+//     that change every instruction the 16 x 16 x 32 form sustains a ~10%
+//     higher clock than 32 x 32 x 16 at the same rate per clock;
+//   * the MFMAs are inline assembly with the accumulators tied to AGPRs ("+a"):
+//     the compiler's own register assignment for this MFMA copies accumulators
+//     between instructions.  Their results are read only after the K loop,
+//     past explicit wait states (the compiler pads its own reads of MFMA
+//     results, not those of inline assembly);
 //   * operand tiles go global -> LDS with buffer_load ... lds (16 bytes per
 //     lane, no staging registers; out-of-range reads return 0 instead of
 //     faulting).  The DMA writes lane i at base + 16 i, so the LDS swizzle is
 //     produced by choosing which global chunk each lane fetches;
 //   * an operand whose rows are K-contiguous in memory is stored as
-//     [256 rows][64 k] and read with ds_read_b128;
+//     [256 rows][64 k] and read with ds_read_b128 (16 rows of one 16-byte
+//     chunk per 16 lanes);
 //   * an operand whose rows are M/N-contiguous (row-major B, transposed A) is
 //     stored as [64 k][256 mn] (512-byte rows) and read with
 //     ds_read_b64_tr_b16: in each 16-lane group, source lane s points at row
 //     k + s/4, column n + 4 (s % 4), and every lane receives 4 consecutive k
-//     of its own column, which is the MFMA fragment layout;
-//   * both swizzles are free of bank conflicts for 32 banks x 4 bytes and for
-//     64 banks x 4 bytes (the XOR patterns below are checked for both);
-//   * two LDS stages, each a distinct LDS object; BK = 64 is four 16-k
-//     substeps.  Fragments are read two substeps ahead into four register
-//     buffers, so every read of a stage is issued by the end of its step's
-//     second substep and the one raw s_barrier per K step sits before the
-//     third: substeps 2-3 issue the DMA for step + 2 (into the stage just
-//     released) and the first two substeps' reads of step + 1.  Reading two
-//     substeps ahead absorbs the delay that the DMA's LDS writes add to the
-//     fragment reads (a scratch build without those writes ran 32% faster);
-//   * fragment addresses are one lane base per operand with the substep and
-//     block folded in as XOR / immediate offsets (equal to kc_off / mc_off);
-//   * the MFMA computes the tile of C^T (B fragment as the first operand) so
+//     of its own column; two such reads give a lane the 8 k of its fragment;
+//   * both swizzles are free of bank conflicts for the reads above;
+//   * two LDS stages, each a distinct LDS object.  The fragments of a substep
+//     are read during the first half of the previous substep into the other
+//     of two register buffers, so every read of a stage is issued within its
+//     step's first substep and the one raw s_barrier per K step sits between
+//     the two; the second substep issues the DMA for step + 2 into the stage
+//     just released.  MFMAs, reads and DMA instructions are placed in a fixed
+//     order (scheduling fences between slots);
+//   * the MFMA computes tiles of C^T (B fragment as the first operand) so
 //     each lane holds 4 consecutive columns of one row of C; the epilogue
 //     stages each wave's 128 x 128 result in LDS and writes 256-byte row
-//     runs with streaming stores (8192^3: +4%; 4096 x 16384 x 4096: +17%);
+//     runs with streaming stores;
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
 //     dispatch over 8 XCDs) form a compact group of C tiles sharing L2;
 //   * partial tiles: rows of a K-contiguous operand past M or N lie past
@@ -74,12 +80,13 @@ __device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t chunk) {
   return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
 }
 // MN-contiguous tile [BK k][256 mn]: byte offset of (k, 16-byte chunk along
-// mn).  A transposed read covers rows k..k+3 (k % 4 == 0) and 4 chunks (32
-// lanes); the XOR values {0, 6, 12, 10} give the four rows distinct 64-byte
-// blocks and, within one 16-lane group, distinct 32-byte units.
+// mn).  A transposed fragment read covers rows 32 s + 8 g + 4 h + {0..3}
+// (g = lane / 16, 16 rows per instruction) and 32 bytes of each; the XOR
+// 2 x(k), x(k) = (k & 3) | ((k >> 3) & 1) << 2, spreads those 16 rows over
+// the 16 bank groups of 16 bytes twice (two 256-byte cycles, the minimum).
 __device__ __forceinline__ uint32_t mc_off(uint32_t k, uint32_t chunk) {
-  const uint32_t t = k & 3u;
-  return k * 512u + ((chunk ^ ((t << 1) ^ (t << 2))) << 4);
+  const uint32_t x = (k & 3u) | (((k >> 3) & 1u) << 2);
+  return k * 512u + ((chunk ^ (x << 1)) << 4);
 }
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset,
@@ -121,52 +128,36 @@ __device__ __forceinline__ void tile_offsets(uint32_t wave, uint32_t lane, uint3
       const uint32_t phys = lane % 32;
       const uint32_t chunk = (mc_off(k, phys) - k * 512u) >> 4;
       // mn_limit: columns of this tile inside the operand (rows past K, on
-      // the last step only, are masked by issue_tile_mn_tail).
+      // the last step only, are masked by issue_one).
       voff[j] = chunk * 8 < mn_limit ? (k * ld + chunk * 8) * 2 : kPadOffset;
     }
   }
 }
 
-template <int BK>
-__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
-                                           uint32_t wave, const uint32_t* voff, uint32_t soffset) {
-#pragma unroll
-  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j)
-    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024, voff[j], soffset);
-}
-
-// The last K step of a K-contiguous operand when K % BK != 0: chunks whose
-// k range starts at or past k_limit (the step's valid k count) read 0.
-template <int BK>
-__device__ __forceinline__ void issue_tile_k_tail(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
-                                                  uint32_t wave, uint32_t lane, const uint32_t* voff,
-                                                  uint32_t soffset, uint32_t k_limit) {
+// DMA instruction j of this wave for one operand tile.  On the last K step
+// when K % BK != 0 (k_limit = the step's valid k count, else 0), the chunks
+// of a K-contiguous row whose k range starts at or past k_limit, or the rows
+// of an MN-contiguous tile at or past k_limit, get an offset past the range
+// and read 0: the step's K offset travels in the scalar offset, which the
+// descriptor's range check does not cover, so rows past K cannot be left to
+// the range of the vector offset alone (they would read the memory after the
+// operand).
+template <int BK, bool KContig>
+__device__ __forceinline__ void issue_one(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile, uint32_t wave,
+                                          uint32_t lane, uint32_t voff, uint32_t j, uint32_t soffset,
+                                          uint32_t k_limit) {
   constexpr int kChunks = BK / 8;
-#pragma unroll
-  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
-    const uint32_t row = (wave * Tile<BK>::kDmaPerWave + j) * (1024 / (BK * 2)) + lane / kChunks;
-    const uint32_t chunk = (kc_off<BK>(row, lane % kChunks) - row * (BK * 2)) >> 4;
-    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024,
-          chunk * 8 < k_limit ? voff[j] : kPadOffset, soffset);
+  const uint32_t inst = wave * Tile<BK>::kDmaPerWave + j;
+  if (k_limit != 0) {
+    if constexpr (KContig) {
+      const uint32_t row = inst * (1024 / (BK * 2)) + lane / kChunks;
+      const uint32_t chunk = (kc_off<BK>(row, lane % kChunks) - row * (BK * 2)) >> 4;
+      voff = chunk * 8 < k_limit ? voff : kPadOffset;
+    } else {
+      voff = inst * 2 + lane / 32 < k_limit ? voff : kPadOffset;  // as tile_offsets
+    }
   }
-}
-
-// The last K step of an MN-contiguous operand when K % BK != 0: tile rows k
-// at or past k_limit get an offset past the range and read 0.  The step's K
-// offset travels in the scalar offset, which the descriptor's range check
-// does not cover, so rows past K cannot be left to the range of the vector
-// offset alone: they would read the memory after the operand.
-template <int BK>
-__device__ __forceinline__ void issue_tile_mn_tail(__amdgpu_buffer_rsrc_t rsrc, uint8_t* tile,
-                                                   uint32_t wave, uint32_t lane,
-                                                   const uint32_t* voff, uint32_t soffset,
-                                                   uint32_t k_limit) {
-#pragma unroll
-  for (uint32_t j = 0; j < (uint32_t)Tile<BK>::kDmaPerWave; ++j) {
-    const uint32_t k = (wave * Tile<BK>::kDmaPerWave + j) * 2 + lane / 32;  // as tile_offsets
-    dma16(rsrc, tile + (wave * Tile<BK>::kDmaPerWave + j) * 1024,
-          k < k_limit ? voff[j] : kPadOffset, soffset);
-  }
+  dma16(rsrc, tile + inst * 1024, voff, soffset);
 }
 
 // fp16 result of one accumulator; with Gelu, GELU of that fp16 value (the
@@ -183,6 +174,12 @@ __device__ __forceinline__ half_t epilogue(float acc) {
 // multiple of 64) and writes its fp32 partial tile to out viewed as
 // float[splits][batches][M][N] (ipu_stack_gemm_f16_split); otherwise
 // k_chunk == K and out is the fp16 C.
+// acc += a . b on one 16 x 16 x 32 tile (a: the first operand's 16 rows, b:
+// the second's 16 columns), the accumulator tied to AGPRs.
+__device__ __forceinline__ void mfma16(float4_t& acc, half8_t a, half8_t b) {
+  asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
 template <bool TransposeLeft, bool TransposeRight, bool Gelu, bool KTail, bool Split>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
@@ -246,133 +243,104 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 
   const uint32_t wm = (wave / 2) * 128, wn = (wave % 2) * 128;
 
-  float16_t acc[4][4];
+  float4_t acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int j = 0; j < 8; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const uint32_t ksteps = (k_len + BK - 1) / BK;
   // K-contiguous operands mask the chunks past K on the last step (MN-
   // contiguous rows past K are past the buffer's range).
   const uint32_t k_tail = k_len % BK;  // nonzero only on the last split
   auto clamp = [&](uint32_t k) { return k < ksteps ? k : ksteps - 1; };
-  // KTail (K % BK != 0) is a separate instantiation, so the branch never
-  // enters the scheduled K loop of the common case.
-  auto issue_a = [&](uint8_t* ta, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && k_tail != 0 && k == ksteps - 1) {
-      if constexpr (kAK)
-        issue_tile_k_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
-      else
-        issue_tile_mn_tail<BK>(a_rsrc, ta, wave, lane, a_voff, k * a_kstep, k_tail);
-    } else
-      issue_tile<BK>(a_rsrc, ta, wave, a_voff, k * a_kstep);
+  // KTail (K % BK != 0) is a separate instantiation, so the tail test never
+  // enters the K loop of the common case.
+  auto limit = [&](uint32_t k) { return KTail && k == ksteps - 1 ? k_tail : 0u; };
+  auto dma_a = [&](uint8_t* ta, uint32_t k, uint32_t j) __attribute__((always_inline)) {
+    issue_one<BK, kAK>(a_rsrc, ta, wave, lane, a_voff[j], j, k * a_kstep, limit(k));
   };
-  auto issue_b = [&](uint8_t* tb, uint32_t k) __attribute__((always_inline)) {
-    if (KTail && k_tail != 0 && k == ksteps - 1) {
-      if constexpr (kBK_)
-        issue_tile_k_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
-      else
-        issue_tile_mn_tail<BK>(b_rsrc, tb, wave, lane, b_voff, k * b_kstep, k_tail);
-    } else
-      issue_tile<BK>(b_rsrc, tb, wave, b_voff, k * b_kstep);
+  auto dma_b = [&](uint8_t* tb, uint32_t k, uint32_t j) __attribute__((always_inline)) {
+    issue_one<BK, kBK_>(b_rsrc, tb, wave, lane, b_voff[j], j, k * b_kstep, limit(k));
   };
-  auto fetch = [&](uint8_t* ta, uint8_t* tb, uint32_t k) {
-    issue_a(ta, k);
-    issue_b(tb, k);
+  auto fetch = [&](uint8_t* ta, uint8_t* tb, uint32_t k) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t j = 0; j < (uint32_t)kDma; ++j) dma_a(ta, k, j);
+#pragma unroll
+    for (uint32_t j = 0; j < (uint32_t)kDma; ++j) dma_b(tb, k, j);
   };
   // Prologue: K steps 0 and 1 (clamped: K = 64 re-fetches step 0 into a
   // stage that is never read).
   fetch(lds_a0, lds_b0, 0);
   fetch(lds_a1, lds_b1, clamp(1));
 
-  // Fragment addresses from per-lane bases (equal to kc_off / mc_off):
-  // K-contiguous rows w0 + 32 i + lane % 32, chunk 2 ks + lane / 32:
-  //   (kbase ^ ((2 ks ^ 4 (i & 1)) << 4)) + 4096 i;
-  // MN-contiguous transposed reads for column block j, substep ks, high half:
-  //   (mbase ^ 64 j) + 8192 ks + 2048 hi.
+  // Fragment addresses from per-lane bases (equal to kc_off / mc_off),
+  // r = lane % 16, g = lane / 16.  K-contiguous tile t (rows w0 + 16 t + r),
+  // substep s (chunk 4 s + g):
+  //   (kbase ^ ((4 s ^ (2 t & 7)) << 4)) + 2048 t;
+  // MN-contiguous tile t (columns w0 + 16 t + ..), substep s, half h (rows
+  // 32 s + 8 g + 4 h + r / 4):
+  //   (mbase ^ (t << 5)) + 16384 s + 2048 h.
+  const uint32_t r16 = lane % 16, g4 = lane / 16;
   auto k_base = [&](uint32_t w0) {
-    const uint32_t b = lane / 32, s0 = (lane & 7) ^ ((lane % 32) / 8);
-    return (w0 + lane % 32) * 128 + ((b ^ s0) << 4);
+    return (w0 + r16) * 128 + ((g4 ^ (r16 & 7) ^ (r16 >> 3)) << 4);
   };
   auto m_base = [&](uint32_t w0) {
-    const uint32_t group = lane / 16, s = lane % 16, t = s / 4;
-    const uint32_t sw = (t << 1) ^ (t << 2), c_l = 2 * (group % 2) + (s % 4) / 2;
-    const uint32_t mn0 = w0 + (group % 2) * 16 + 4 * (s % 4);
-    return ((group / 2) * 8 + t) * 512 + (w0 / 8) * 16 + 16 * (c_l ^ (sw & 3)) + (mn0 % 8) * 2 +
-           64 * ((sw >> 2) & 3);
+    const uint32_t r4 = r16 / 4, c1 = (r16 % 4) / 2, xr = r4 | ((g4 & 1) << 2);
+    return (8 * g4 + r4) * 512 + 2 * w0 + 16 * c1 + 8 * (r16 % 2) + (xr << 5);
   };
   const uint32_t a_base_l = kAK ? k_base(wm) : m_base(wm);
   const uint32_t b_base_l = kBK_ ? k_base(wn) : m_base(wn);
-  auto frag = [&]<bool KContig>(const uint8_t* tile, uint32_t base, int blk, int ks) __attribute__((always_inline)) {
+  auto frag = [&]<bool KContig>(const uint8_t* tile, uint32_t base, int t, int s) __attribute__((always_inline)) {
     if constexpr (KContig) {
       return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(
-                                             tile + ((base ^ (((2 * ks) ^ (4 * (blk & 1))) << 4)) + 4096 * blk)));
+                                             tile + ((base ^ (((4 * s) ^ ((2 * t) & 7)) << 4)) + 2048 * t)));
     } else {
-      const uint32_t a = (base ^ (64 * blk)) + 8192 * ks;
+      const uint32_t a = (base ^ (t << 5)) + 16384 * s;
       const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a));
       const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a + 2048));
       return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
 
-  // Four fragment buffers: substep s multiplies buffer s and its reads fill
-  // buffer (s + 2) % 4, two substeps ahead.  Every read of a stage is then
-  // issued by the end of its step's substep 1, so the per-step barrier sits
-  // before substep 2; the DMA of step kt + 2 goes into the stage just
-  // released during substeps 2-3 and has four substeps to land.
-  half8_t fa[4][4], fb[4][4];
-  constexpr int kDsPerSub = (kAK ? 4 : 8) + (kBK_ ? 4 : 8);
-  auto read_sub = [&](const uint8_t* ta, const uint8_t* tb, int ks, int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[buf][i] = frag.template operator()<kAK>(ta, a_base_l, i, ks);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) fb[buf][j] = frag.template operator()<kBK_>(tb, b_base_l, j, ks);
+  half8_t fa[2][8], fb[2][8];
+  // Fragment item r of a substep: r < 8 is B tile r, r >= 8 is A tile r - 8
+  // (the order in which that substep's MFMAs first use them).
+  auto read_item = [&](const uint8_t* ta, const uint8_t* tb, int s, int buf, int r) __attribute__((always_inline)) {
+    if (r < 8) fb[buf][r] = frag.template operator()<kBK_>(tb, b_base_l, r, s);
+    else fa[buf][r - 8] = frag.template operator()<kAK>(ta, a_base_l, r - 8, s);
   };
-  auto mma = [&](int buf) __attribute__((always_inline)) {
+  // One substep: the 64 MFMAs of register buffer buf; after every second
+  // MFMA of the first 32, one fragment of the next substep (into buffer
+  // 1 - buf); with dma_k >= 0, the step's 2 x kDma DMA instructions after
+  // every fourth MFMA.  Fences keep this order.
+  auto substep = [&](int buf, const uint8_t* ra, const uint8_t* rb, int rs, uint8_t* da, uint8_t* db,
+                     int64_t dma_k) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
-  };
-  auto sched = [&](int dma) __attribute__((always_inline)) {
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (m < kDsPerSub) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (m < dma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    for (int m = 0; m < 64; ++m) {
+      const int i = m / 8, j = m % 8;
+      mfma16(acc[i][j], fb[buf][j], fa[buf][i]);
+      if (m < 32 && m % 2 == 1) read_item(ra, rb, rs, 1 - buf, m / 2);
+      if (dma_k >= 0 && m % 4 == 1) {
+        const int d = m / 4;
+        if (d < kDma) dma_a(da, (uint32_t)dma_k, d);
+        else dma_b(db, (uint32_t)dma_k, d - kDma);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  read_sub(lds_a0, lds_b0, 0, 0);
-  read_sub(lds_a0, lds_b0, 1, 1);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) read_item(lds_a0, lds_b0, 0, 0, r);
   auto step = [&](uint8_t* ta, uint8_t* tb, const uint8_t* na, const uint8_t* nb, uint32_t kt)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    read_sub(ta, tb, 2, 2);
-    mma(0);
-    sched(0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_sub(ta, tb, 3, 3);
-    mma(1);
-    sched(0);
-    __builtin_amdgcn_sched_barrier(0);
+    substep(0, ta, tb, 1, nullptr, nullptr, -1);
     // This wave's reads of (ta, tb) have returned and its DMA of step kt + 1
     // has landed; after the barrier, every wave's have.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue_a(ta, clamp(kt + 2));
-    read_sub(na, nb, 0, 0);
-    mma(2);
-    sched(kDma);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_b(tb, clamp(kt + 2));
-    read_sub(na, nb, 1, 1);
-    mma(3);
-    sched(kDma);
+    substep(1, na, nb, 0, ta, tb, (int64_t)clamp(kt + 2));
   };
 
   uint32_t kt = 0;
@@ -382,51 +350,45 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   }
   if (kt < ksteps) step(lds_a0, lds_b0, lds_a1, lds_b1, kt);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the redundant prefetches
+  // 24 wait states before any read of the accumulators (see mfma16).
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
+  // acc[i][j][e] = C[m0 + wm + 16 i + lane % 16][n0 + wn + 16 j + 4 (lane / 16) + e]
   if constexpr (Split) {
     // fp32 partial tile, 16-byte stores of 4 consecutive columns.
     float* P = reinterpret_cast<float*>(out) +
                ((uint64_t)blockIdx.z * gridDim.y + batch) * (uint64_t)M * N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t row = m0 + wm + 32 * i + lane % 32;
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t row = m0 + wm + 16 * i + r16;
       if (row >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t col = n0 + wn + 32 * j + 8 * g + 4 * (lane / 32);
-          if (col >= N) continue;
-          float4_t v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
-          __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(P + (uint64_t)row * N + col));
-        }
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t col = n0 + wn + 16 * j + 4 * g4;
+        if (col >= N) continue;
+        __builtin_nontemporal_store(acc[i][j], reinterpret_cast<float4_t*>(P + (uint64_t)row * N + col));
+      }
     }
     return;
   }
 
   // The wave's 128 x 128 fp16 result goes through its own quarter of the
   // (now idle) LDS stages, so that it reaches memory as 256-byte row runs
-  // written by 16 lanes with streaming stores instead of 16-byte pieces of
-  // 32 rows per instruction.  Layout: row r (256 bytes), 16-byte chunk c at
+  // written by 16 lanes with streaming stores instead of 8-byte pieces of
+  // 16 rows per instruction.  Layout: row r (256 bytes), 16-byte chunk c at
   // chunk c ^ (r & 15).
-  // acc[i][j][r] = C[m0 + wm + 32 i + lane % 32][n0 + wn + 32 j + 8 (r / 4) + 4 (lane / 32) + r % 4]
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
   uint8_t* cst = wave == 0 ? lds_a0 : wave == 1 ? lds_b0 : wave == 2 ? lds_a1 : lds_b1;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = 32 * i + lane % 32;
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t r = 16 * i + r16;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
+      half4_t h;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        half4_t h;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = epilogue<Gelu>(acc[i][j][4 * g + e]);
-        const uint32_t c = 4 * j + g;
-        *reinterpret_cast<half4_t*>(cst + r * 256 + ((c ^ (r & 15)) << 4) + (lane / 32) * 8) = h;
-      }
+      for (int e = 0; e < 4; ++e) h[e] = epilogue<Gelu>(acc[i][j][e]);
+      const uint32_t c = 2 * j + g4 / 2;
+      *reinterpret_cast<half4_t*>(cst + r * 256 + ((c ^ (r & 15)) << 4) + (g4 % 2) * 8) = h;
     }
   }
   uint16_t* cw = C + (uint64_t)(m0 + wm) * N + n0 + wn;
