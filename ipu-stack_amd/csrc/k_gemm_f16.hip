@@ -30,7 +30,8 @@
 //     ds_read_b64_tr_b16: in each 16-lane group, source lane s points at row
 //     k + s/4, column n + 4 (s % 4), and every lane receives 4 consecutive k
 //     of its own column; two such reads give a lane the 8 k of its fragment;
-//   * both swizzles are free of bank conflicts for the reads above;
+//   * both swizzles are free of bank conflicts for the reads above
+//     (SQ_LDS_BANK_CONFLICT checked per layout);
 //   * two LDS stages, each a distinct LDS object.  The fragments of a substep
 //     are read during the first half of the previous substep into the other
 //     of two register buffers, so every read of a stage is issued within its
@@ -71,13 +72,15 @@ typedef short short4_t __attribute__((vector_size(8)));
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
 // K-contiguous tile [256 rows][BK k]: byte offset of (row, 16-byte chunk).
-// A b128 fragment read touches 16 consecutive rows of one chunk per 256-byte
-// (64-bank) cycle, 8 per 128-byte (32-bank) cycle; the row-dependent XOR puts
-// them in distinct bank groups under both.
+// A fragment read covers 16 consecutive rows and, per 16-lane group, one
+// chunk (4 chunks per instruction); XOR-ing the chunk with the row's low 3
+// bits reads without bank conflicts (SQ_LDS_BANK_CONFLICT = 0 in a probe of
+// this pattern; the XOR with (row ^ row >> 3) & 7 that suits 32-row reads
+// costs 4 conflict cycles per read here).
 template <int BK>
 __device__ __forceinline__ uint32_t kc_off(uint32_t row, uint32_t chunk) {
   static_assert(BK == 64, "128-byte rows, 8 chunks");
-  return row * 128u + ((chunk ^ ((row ^ (row >> 3)) & 7u)) << 4);
+  return row * 128u + ((chunk ^ (row & 7u)) << 4);
 }
 // MN-contiguous tile [BK k][256 mn]: byte offset of (k, 16-byte chunk along
 // mn).  A transposed fragment read covers rows 32 s + 8 g + 4 h + {0..3}
@@ -277,13 +280,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   // Fragment addresses from per-lane bases (equal to kc_off / mc_off),
   // r = lane % 16, g = lane / 16.  K-contiguous tile t (rows w0 + 16 t + r),
   // substep s (chunk 4 s + g):
-  //   (kbase ^ ((4 s ^ (2 t & 7)) << 4)) + 2048 t;
+  //   (kbase ^ (64 s)) + 2048 t;
   // MN-contiguous tile t (columns w0 + 16 t + ..), substep s, half h (rows
   // 32 s + 8 g + 4 h + r / 4):
   //   (mbase ^ (t << 5)) + 16384 s + 2048 h.
   const uint32_t r16 = lane % 16, g4 = lane / 16;
   auto k_base = [&](uint32_t w0) {
-    return (w0 + r16) * 128 + ((g4 ^ (r16 & 7) ^ (r16 >> 3)) << 4);
+    return (w0 + r16) * 128 + ((g4 ^ (r16 & 7)) << 4);
   };
   auto m_base = [&](uint32_t w0) {
     const uint32_t r4 = r16 / 4, c1 = (r16 % 4) / 2, xr = r4 | ((g4 & 1) << 2);
@@ -293,8 +296,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   const uint32_t b_base_l = kBK_ ? k_base(wn) : m_base(wn);
   auto frag = [&]<bool KContig>(const uint8_t* tile, uint32_t base, int t, int s) __attribute__((always_inline)) {
     if constexpr (KContig) {
-      return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(
-                                             tile + ((base ^ (((4 * s) ^ ((2 * t) & 7)) << 4)) + 2048 * t)));
+      return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(tile + ((base ^ (64 * s)) + 2048 * t)));
     } else {
       const uint32_t a = (base ^ (t << 5)) + 16384 * s;
       const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a));
