@@ -9,33 +9,36 @@
 //
 // Fast kernel (width == value width, a multiple of 8 up to 128, computed in
 // tiles 64 or 128 columns wide with zero padding):
-//   * 256 threads = 4 waves; a wave owns 32 queries, a workgroup 128 queries
-//     of one stream; two workgroups share a CU (launch bound), so one SIMD
-//     runs the softmax of one wave while the MFMA pipe serves the other;
+//   * 256 threads = 4 waves; a wave owns 32 queries (two tiles of 16), a
+//     workgroup 128 queries of one stream; two workgroups share a CU (launch
+//     bound), so one SIMD runs the softmax of one wave while the MFMA pipe
+//     serves the other;
 //   * keys stream through LDS in blocks of 64 with two stages.  K and V tiles
 //     are copied global -> LDS with buffer_load ... lds (16 bytes per lane, no
 //     staging registers; rows past the end of the stream read as 0), both
 //     stored row-major [64 keys][D] with an XOR swizzle of 16-byte chunks;
+//   * v_mfma_f32_16x16x32_f16 throughout: under the board's power limit it
+//     sustains a higher clock than 32 x 32 x 16 on changing operands;
 //   * software pipeline: step j runs ONE MFMA cluster holding the scores of
 //     block j and the output update of block j - 1 (alternating, fragments
 //     read ahead, the step's DMA instructions spread between them), then the
 //     softmax of block j on the VALU.  K tiles run one block ahead of V;
-//   * scores are computed transposed, S^T = K Q^T, with
-//     v_mfma_f32_32x32x16_f16 (K fragments by ds_read_b128 as the first
-//     operand, Q fragments resident in registers as the second), so a lane
-//     holds 32 keys of ONE query: the row max needs one exchange (lane ^ 32)
-//     and the running sum none until the end;
+//   * scores are computed transposed, S^T = K Q^T (K fragments by
+//     ds_read_b128 as the first operand, Q fragments resident in registers
+//     as the second), so a lane holds 4 consecutive keys of one query per
+//     16 x 16 tile: four lanes share a query, whose max needs two exchanges
+//     and whose running sum none until the end;
 //   * the output is accumulated transposed, O^T += V^T P^T: the fp16
 //     probabilities are the second MFMA operand straight from the score
 //     registers, and the matching V^T fragments come from the row-major V
 //     tile through ds_read_b64_tr_b16, whose 4-key runs are chosen to follow
 //     the score accumulator's key order;
+//   * each fragment read feeds two MFMAs (the wave's two query tiles);
 //   * the reference point (running max) moves only when some probability of
 //     a block would exceed 2^kRescaleSlack, which the block's probability
 //     sum bounds, so no max over the scores is taken on the common path:
 //     the result is exact for any reference point, and most blocks skip the
-//     max, the rescale of the output accumulators and the exchange with the
-//     partner lane;
+//     max, the rescale of the output accumulators and the lane exchanges;
 //   * K and V fragment offsets are computed once per lane (XOR swizzles of
 //     one base), so the cluster's LDS reads take immediate offsets only;
 //   * causal: key blocks past the workgroup's last query are never loaded, a
@@ -67,9 +70,12 @@ typedef short short4_t __attribute__((vector_size(8)));
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
 // Tiles of 64 keys x D fp16, rows of D * 2 bytes, 16-byte chunks swizzled by
-// row.  K is read with ds_read_b128 (16 consecutive rows, one chunk, per
-// 256-byte cycle); V with ds_read_b64_tr_b16 (4 consecutive rows x 4 chunks
-// per 32 lanes).  The XORs give each of those reads distinct banks.
+// row.  K is read with ds_read_b128 (each 16-lane group: 16 consecutive rows
+// of one chunk), V with ds_read_b64_tr_b16 (each 16-lane group: 4 consecutive
+// rows x 32 bytes, 16 consecutive rows per instruction).  The XORs below read
+// both without bank conflicts (SQ_LDS_BANK_CONFLICT = 0 in a probe of the two
+// patterns; they depend only on the row's low bits, which a DMA step of
+// kThreads / kChunks rows leaves alone).
 template <int D>
 struct KvTile {
   static constexpr uint32_t kRowBytes = D * 2;
@@ -79,28 +85,24 @@ struct KvTile {
 };
 template <int D>
 __device__ __forceinline__ uint32_t k_swz(uint32_t row) {
-  return D == 128 ? (row & 15u) : ((row >> 1) & 7u);
+  return D == 128 ? (row & 15u) : (row & 7u);
 }
 template <int D>
 __device__ __forceinline__ uint32_t v_swz(uint32_t row) {
-  return D == 128 ? ((row & 3u) << 2) : (((row >> 1) & 1u) << 2);
-}
-template <int D>
-__device__ __forceinline__ uint32_t k_off(uint32_t row, uint32_t chunk) {
-  return row * KvTile<D>::kRowBytes + ((chunk ^ k_swz<D>(row)) << 4);
-}
-template <int D>
-__device__ __forceinline__ uint32_t v_off(uint32_t row, uint32_t chunk) {
-  return row * KvTile<D>::kRowBytes + ((chunk ^ v_swz<D>(row)) << 4);
+  return D == 128 ? ((row & 7u) << 1) : (row & 7u);
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-// max / sum of x over lanes l and l ^ 32 (one ds_bpermute exchange).
-__device__ __forceinline__ float max_with_partner(float x) {
+// max / sum of x over the four lanes l ^ {0, 16, 32, 48} that hold one query.
+__device__ __forceinline__ float max_of_query(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, kWave));
   return fmaxf(x, __shfl_xor(x, 32, kWave));
 }
-__device__ __forceinline__ float sum_with_partner(float x) { return x + __shfl_xor(x, 32, kWave); }
+__device__ __forceinline__ float sum_of_query(float x) {
+  x += __shfl_xor(x, 16, kWave);
+  return x + __shfl_xor(x, 32, kWave);
+}
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)lds, 16, voffset, 0, 0, 0);
@@ -131,11 +133,13 @@ __device__ __forceinline__ void attention_block(
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
     uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
     uint32_t v_heads) {
-  constexpr uint32_t kDT = D / 32;  // output d tiles
-  constexpr uint32_t kKS = D / 16;  // k steps of the score MFMA
+  constexpr uint32_t kKS = D / 32;  // k steps (32 columns) of the score MFMAs
+  constexpr uint32_t kDT = D / 16;  // output d tiles (16 columns)
+  constexpr uint32_t kPairs = 4 * kKS;  // score MFMA pairs (query tiles 0, 1) per key block
+  constexpr uint32_t kRB = KvTile<D>::kRowBytes;
   constexpr uint32_t kTile = KvTile<D>::kBytes;
   constexpr uint32_t kDmaRows = kThreads / KvTile<D>::kChunks;  // rows per DMA instruction
-  static_assert(4 * kDT == 2 * kKS, "one PV MFMA per score MFMA");
+  static_assert(kPairs == 2 * kDT, "one output MFMA pair per score MFMA pair");
   // Two stages, each a distinct LDS object so the compiler can see that the
   // DMA into one stage never aliases the fragment reads of the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTile];
@@ -145,6 +149,7 @@ __device__ __forceinline__ void attention_block(
 
   const uint32_t q0 = qb * kQueriesPerBlock;
   const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t r16 = lane % 16, g4 = lane / 16;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const uint32_t wq0 = q0 + wave_s * kQueriesPerWave;  // first query of this wave
 
@@ -179,69 +184,70 @@ __device__ __forceinline__ void attention_block(
     nproc = lim < nproc ? lim : nproc;
   }
 
-  // Q fragments (second MFMA operand): lane holds Q[q][16 ks + 8 (lane/32) ..+7].
-  half8_t qf[kKS];
-  {
-    uint32_t q = wq0 + lane % 32;
+  // The wave's 32 queries are two tiles of 16 (qt); lane l serves query
+  // wq0 + 16 qt + l % 16 of each.  Q fragments (second MFMA operand of the
+  // scores) for tile qt, k step ks: Q[query][32 ks + 8 (l / 16) .. +7].
+  half8_t qf[2][kKS];
+#pragma unroll
+  for (uint32_t qt = 0; qt < 2; ++qt) {
+    uint32_t q = wq0 + 16 * qt + r16;
     q = q < query_rows ? q : query_rows - 1;
 #pragma unroll
-    for (uint32_t ks = 0; ks < kKS; ++ks)
-    {
-      const uint32_t d0 = ks * 16 + (lane / 32) * 8;  // padding columns are 0
-      qf[ks] = __builtin_bit_cast(
+    for (uint32_t ks = 0; ks < kKS; ++ks) {
+      const uint32_t d0 = ks * 32 + g4 * 8;  // padding columns are 0
+      qf[qt][ks] = __builtin_bit_cast(
           half8_t, d0 < width ? load16(Q + (uint64_t)q * q_pitch + d0) : u32x4{0, 0, 0, 0});
     }
   }
 
-  float16_t o[kDT];
+  float4_t o[kDT][2];
 #pragma unroll
   for (uint32_t dt = 0; dt < kDT; ++dt)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
-  float m_run = -INFINITY;  // reference point, log2 units (scaled)
-  float l_run = 0.0f;       // this lane's share of the row sum
-  half8_t pp[2][2];         // fp16 probabilities of the last softmax
+    for (uint32_t qt = 0; qt < 2; ++qt) o[dt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run[2] = {-INFINITY, -INFINITY};  // reference points, log2 units (scaled)
+  float l_run[2] = {0.0f, 0.0f};            // this lane's share of the row sums
+  half8_t pp[2][2];  // fp16 probabilities of the last softmax [key half kk][qt]
 #pragma unroll
-  for (int st = 0; st < 2; ++st)
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pp[st][h][e] = (half_t)0.0f;  // "block -1"
-  const uint32_t qi = wq0 + lane % 32;
+      for (int e = 0; e < 8; ++e) pp[kk][qt][e] = (half_t)0.0f;  // "block -1"
+  uint32_t qi[2] = {wq0 + r16, wq0 + 16 + r16};
 
-  // Fragment reads.  K fragment (first operand of S^T = K Q^T): lane holds
-  // K[32 st + lane % 32][16 ks + 8 (lane / 32) .. +7].  V^T fragment (first
-  // operand of O^T += V^T P^T) for d tile dt and keys 32 st + 16 h + {0..15}:
-  // lane holds d = 32 dt + lane % 32 and, in element e, key 32 st + 16 h +
-  // 8 (e / 4) + 4 (lane / 32) + e % 4, the key order of score accumulator
-  // elements 8 h .. 8 h + 7; each ds_read_b64_tr_b16 returns 4 consecutive
-  // keys (in a 16-lane group, source lane s addresses row key0 + s / 4,
-  // columns d0 + 4 (s % 4) .. +3).  Offsets are those of the first rows
-  // XORed with the k step (chunk 2 ks: bits 5..) or d tile (chunk 4 dt: bits
-  // 6..), since both swizzles XOR the chunk with row bits; other rows add a
-  // constant (an immediate offset of the LDS read).  The per-k-step and
-  // per-d-tile offsets are computed once and stay in registers.
-  const uint32_t kbase = k_off<D>(lane % 32, lane / 32);
+  // Score accumulator s[kt][qt] (v_mfma_f32_16x16x32_f16 of K tile kt as the
+  // first operand): element e is key 16 kt + 4 (l / 16) + e of query qt.
+  // Output MFMAs contract 32 keys (half kk of the block): k slot 8 (l / 16) + e
+  // is key 32 kk + 4 (l / 16) + e for e < 4 and 32 kk + 16 + 4 (l / 16) + e - 4
+  // otherwise, which is how pp packs the score elements, so each lane's
+  // probabilities feed the MFMA where they are.
+  // K fragment for key tile kt, k step ks: lane holds K[16 kt + l % 16][32 ks
+  // + 8 (l / 16) .. +7] (ds_read_b128).  V^T fragment for d tile dt and half
+  // kk: lane holds d = 16 dt + l % 16 of the 8 keys of its k slots, two
+  // ds_read_b64_tr_b16 of 4 consecutive keys each (in a 16-lane group, source
+  // lane s addresses key k0 + s / 4, columns 16 dt + 4 (s % 4) .. +3).  The
+  // swizzles depend on the row's low bits only, so the offsets are per-lane
+  // bases XORed with the k step or d tile plus an immediate row offset.
+  const uint32_t kbase = r16 * kRB + ((g4 ^ k_swz<D>(r16)) << 4);
   uint32_t vbase;
   {
-    const uint32_t sl = lane % 16, g = lane / 32, dg = (lane / 16) % 2;
-    const uint32_t d = 16 * dg + 4 * (sl % 4);
-    vbase = v_off<D>(4 * g + sl / 4, d / 8) + (d % 8) * 2;
+    const uint32_t row = 4 * g4 + r16 / 4, c1 = (r16 % 4) / 2;
+    vbase = row * kRB + ((c1 ^ v_swz<D>(row)) << 4) + 8 * (r16 % 2);
   }
   uint32_t kofs[kKS], vofs[kDT];
 #pragma unroll
-  for (uint32_t ks = 0; ks < kKS; ++ks) kofs[ks] = kbase ^ (ks << 5);
+  for (uint32_t ks = 0; ks < kKS; ++ks) kofs[ks] = kbase ^ (ks << 6);
 #pragma unroll
-  for (uint32_t dt = 0; dt < kDT; ++dt) vofs[dt] = vbase ^ (dt << 6);
-  auto kfrag = [&](const uint8_t* lk, uint32_t st, uint32_t ks) __attribute__((always_inline)) {
-    const uint8_t* p = lk + kofs[ks] + st * 32 * KvTile<D>::kRowBytes;
+  for (uint32_t dt = 0; dt < kDT; ++dt) vofs[dt] = vbase ^ (dt << 5);
+  auto kfrag = [&](const uint8_t* lk, uint32_t kt, uint32_t ks) __attribute__((always_inline)) {
+    const uint8_t* p = lk + kofs[ks] + 16 * kt * kRB;
     return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(p));
   };
-  auto vfrag = [&](const uint8_t* lv, uint32_t st, uint32_t h, uint32_t dt) __attribute__((always_inline)) {
-    const uint8_t* p = lv + vofs[dt] + (32 * st + 16 * h) * KvTile<D>::kRowBytes;
+  auto vfrag = [&](const uint8_t* lv, uint32_t dt, uint32_t kk) __attribute__((always_inline)) {
+    const uint8_t* p = lv + vofs[dt] + 32 * kk * kRB;
     const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
-    const short4_t hi =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 8 * KvTile<D>::kRowBytes));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kRB));
     return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
@@ -264,57 +270,46 @@ __device__ __forceinline__ void attention_block(
   // scores of block j and the output update of block j - 1 (from pp), with
   // the step's DMA spread over it, then the softmax of block j on the VALU.
   // K tiles run one block ahead of V tiles: step j fetches K(j + 1) and V(j),
-  // each into the stage last read in step j - 1.
-  auto cluster = [&]<bool WithPv>(float16_t* s, const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
+  // each into the stage last read in step j - 1.  Pair p of the cluster is
+  // score pair (k step p / 4, key tile p % 4) and output pair (half p / kDT,
+  // d tile p % kDT), each over query tiles 0 and 1 with one fragment read.
+  auto cluster = [&]<bool WithPv>(float4_t (*s)[2], const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
                                    uint8_t* nv, uint32_t kbi) __attribute__((always_inline)) {
     const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
-    // K and V fragments two k steps ahead (four MFMAs between a fragment's
-    // read and its use, which covers the LDS latency).
+      for (int qt = 0; qt < 2; ++qt) s[kt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // Fragments two pairs ahead.
     constexpr uint32_t kAhead = 2;
-    half8_t kf[kAhead][2], vf[kAhead][2];
-    // PV MFMA n = 2 ks + st of 16: (st, h) pair n / kDT, d tile n % kDT.
-    auto pv_frag = [&](uint32_t ks, uint32_t st) __attribute__((always_inline)) {
-      const uint32_t n = 2 * ks + st, c = n / kDT, dt = n % kDT;
-      return vfrag(lv, c / 2, c % 2, dt);
-    };
+    half8_t kf[kAhead], vf[kAhead];
 #pragma unroll
-    for (uint32_t ks = 0; ks < kAhead; ++ks)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        kf[ks][st] = kfrag(lk, st, ks);
-        if constexpr (WithPv) vf[ks][st] = pv_frag(ks, st);
-      }
+    for (uint32_t p = 0; p < kAhead; ++p) {
+      kf[p] = kfrag(lk, p % 4, p / 4);
+      if constexpr (WithPv) vf[p] = vfrag(lv, p % kDT, p / kDT);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // Raised priority while this wave feeds the matrix pipe: the other wave
     // on the SIMD fills the gaps with its softmax.
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (uint32_t ks = 0; ks < kKS; ++ks) {
+    for (uint32_t p = 0; p < kPairs; ++p) {
+      const uint32_t ks = p / 4, kt = p % 4, kk = p / kDT, dt = p % kDT;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks % kAhead][st], qf[ks], s[st], 0, 0, 0);
-        if constexpr (WithPv) {
-          const uint32_t n = 2 * ks + st, c = n / kDT, dt = n % kDT;
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[ks % kAhead][st], pp[c / 2][c % 2], o[dt],
-                                                         0, 0, 0);
-        }
+      for (int qt = 0; qt < 2; ++qt) {
+        s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[p % kAhead], qf[qt][ks], s[kt][qt], 0, 0, 0);
+        if constexpr (WithPv)
+          o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[p % kAhead], pp[kk][qt], o[dt][qt], 0, 0, 0);
       }
-      if (ks + kAhead < kKS) {
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          kf[ks % kAhead][st] = kfrag(lk, st, ks + kAhead);
-          if constexpr (WithPv) vf[ks % kAhead][st] = pv_frag(ks + kAhead, st);
-        }
+      if (p + kAhead < kPairs) {
+        kf[p % kAhead] = kfrag(lk, (p + kAhead) % 4, (p + kAhead) / 4);
+        if constexpr (WithPv) vf[p % kAhead] = vfrag(lv, (p + kAhead) % kDT, (p + kAhead) / kDT);
       }
-      // DMA instructions spread over the k steps: K tile first, then V.
-      constexpr uint32_t kDmaPer = (2 * KvTile<D>::kDma + kKS - 1) / kKS;
+      // DMA instructions spread over the pairs: K tile first, then V.
+      constexpr uint32_t kDmaPer = (2 * KvTile<D>::kDma + kPairs - 1) / kPairs;
 #pragma unroll
       for (uint32_t u = 0; u < kDmaPer; ++u) {
-        const uint32_t i = ks * kDmaPer + u;
+        const uint32_t i = p * kDmaPer + u;
         if (i < KvTile<D>::kDma) dma_k(i, nk, next * k_block_bytes);
         else if (i < 2 * KvTile<D>::kDma) dma_v(i - KvTile<D>::kDma, nv, kbi * v_block_bytes);
       }
@@ -325,95 +320,105 @@ __device__ __forceinline__ void attention_block(
   // Output update of the previous block alone (V tile lv).
   auto pv_only = [&](const uint8_t* lv) __attribute__((always_inline)) {
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (uint32_t kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (uint32_t dt = 0; dt < kDT; ++dt) {
+        const half8_t v = vfrag(lv, dt, kk);
 #pragma unroll
-        for (uint32_t dt = 0; dt < kDT; ++dt)
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vfrag(lv, st, h, dt), pp[st][h], o[dt], 0, 0, 0);
+        for (int qt = 0; qt < 2; ++qt)
+          o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v, pp[kk][qt], o[dt][qt], 0, 0, 0);
+      }
   };
-  // Softmax of block kbi.  s[st][r] is the score of key kb + 32 st + 8 (r/4)
-  // + 4 (lane/32) + r%4 for query qi; the result goes to pp.
-  auto softmax = [&](float16_t* s, uint32_t kbi) __attribute__((always_inline)) {
+  // Softmax of block kbi.  s[kt][qt][e] is the score of key kb + 16 kt +
+  // 4 (l / 16) + e for query qi[qt]; the result goes to pp.
+  auto softmax = [&](float4_t (*s)[2], uint32_t kbi) __attribute__((always_inline)) {
     const uint32_t kb = kbi * kKeysPerBlock;
     const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
     if (need_mask) {
-      // Key kb + 4 (lane / 32) + x is allowed iff x <= lim (the last allowed
-      // key is min(qi, key_rows - 1) causal, key_rows - 1 otherwise; key_rows
-      // < 2^30, so lim fits an int).
-      const uint32_t last = Causal && qi < key_rows - 1 ? qi : key_rows - 1;
-      const int lim = (int)last - (int)(kb + 4 * (lane / 32));
-      // One compare into VCC and one select per score (compares into SGPR
-      // pairs, as the compiler hoists them, run out of SGPRs).  The scores
-      // come straight from MFMAs, and the hazard padding the compiler gives
-      // its own VALU reads of MFMA results does not cover inline assembly:
-      // 24 wait states first.
+      // Key kb + 4 (l / 16) + x is allowed for query qi iff x <= lim (the
+      // last allowed key is min(qi, key_rows - 1) causal, key_rows - 1
+      // otherwise; key_rows < 2^30, so lim fits an int).  One compare into
+      // VCC and one select per score; the scores come straight from MFMAs,
+      // and the hazard padding the compiler gives its own VALU reads of MFMA
+      // results does not cover inline assembly: 24 wait states first.
+      int lim[2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const uint32_t last = Causal && qi[qt] < key_rows - 1 ? qi[qt] : key_rows - 1;
+        lim[qt] = (int)last - (int)(kb + 4 * g4);
+      }
       const float ninf = -INFINITY;
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          asm volatile("v_cmp_gt_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %0, %3, vcc"
-                       : "+v"(s[st][r])
-                       : "n"(32 * st + 8 * (r / 4) + r % 4), "v"(lim), "v"(ninf)
-                       : "vcc");
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            asm volatile("v_cmp_gt_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %0, %3, vcc"
+                         : "+v"(s[kt][qt][e])
+                         : "n"(16 * kt + e), "v"(lim[qt]), "v"(ninf)
+                         : "vcc");
     }
-    // Probabilities against the current reference point, and this lane's
-    // share of the block's row sum.  The row sum adds the fp16
-    // probabilities that the MFMA consumes: pairs, then quads, in fp16
-    // (each p <= 2^kRescaleSlack on the accepted path, so a quad sum stays
-    // far inside the fp16 range and carries at most two roundings), then
-    // fp32 accumulation with v_dot2.
-    auto exps = [&](float neg_m, half8_t (*pf)[2]) __attribute__((always_inline)) {
-      float sum = 0.0f;
+    // Probabilities against the current reference points, and this lane's
+    // share of each query's block sum: the fp16 probabilities that the MFMA
+    // consumes, added in pairs and quads in fp16 (each p <= 2^kRescaleSlack
+    // on the accepted path, so a quad sum stays far inside the fp16 range
+    // and carries at most two roundings), then accumulated in fp32 by v_dot2.
+    auto exps = [&](const float* neg_m, half8_t (*pf)[2], float* sum) __attribute__((always_inline)) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int qt = 0; qt < 2; ++qt) {
+        sum[qt] = 0.0f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            pf[st][h][e] = (half_t)__builtin_amdgcn_exp2f(fmaf(s[st][8 * h + e], scale_log2, neg_m));
-          const half2_t s01 = half2_t{pf[st][h][0], pf[st][h][1]} + half2_t{pf[st][h][2], pf[st][h][3]};
-          const half2_t s45 = half2_t{pf[st][h][4], pf[st][h][5]} + half2_t{pf[st][h][6], pf[st][h][7]};
-          sum = __builtin_amdgcn_fdot2(s01 + s45, half2_t{1, 1}, sum, false);
+            pf[kk][qt][e] = (half_t)__builtin_amdgcn_exp2f(
+                fmaf(s[2 * kk + e / 4][qt][e % 4], scale_log2, neg_m[qt]));
+          const half2_t s01 = half2_t{pf[kk][qt][0], pf[kk][qt][1]} + half2_t{pf[kk][qt][2], pf[kk][qt][3]};
+          const half2_t s45 = half2_t{pf[kk][qt][4], pf[kk][qt][5]} + half2_t{pf[kk][qt][6], pf[kk][qt][7]};
+          sum[qt] = __builtin_amdgcn_fdot2(s01 + s45, half2_t{1, 1}, sum[qt], false);
         }
-      return sum;
+      }
     };
-    // The reference point moves only when some probability would exceed
+    // A reference point moves only when some probability would exceed
     // 2^kRescaleSlack, found without a max over the scores: every p is at
-    // most the lane's block sum, so a block sum <= 2^kRescaleSlack accepts
-    // the block (overflow to inf and NaN, as against the -inf start, fail
-    // the test).  Otherwise the max of the query's 64 keys (this lane and
-    // its partner lane ^ 32, so both halves share one reference point; it is
-    // finite, as every processed block holds an allowed key per query)
-    // becomes the reference point, the output and sum are rescaled, and the
-    // probabilities are recomputed (all <= 1).  Exact for any reference
-    // point.
+    // most its lane's block sum, so sums <= 2^kRescaleSlack accept the block
+    // (overflow to inf and NaN, as against the -inf start, fail the test).
+    // Otherwise each query's max over its 64 keys (the four lanes that hold
+    // it, so they share one reference point; finite, as every processed block
+    // holds an allowed key per query) becomes its reference point, the
+    // output and sum are rescaled, and the probabilities recomputed (all
+    // <= 1).  Exact for any reference point.
     half8_t pf[2][2];
-    float sum = exps(-m_run, pf);
-    if (__any(!(sum <= kSumLimit))) {
-      float mx = s[0][0];
+    float sum[2];
+    float neg_m[2] = {-m_run[0], -m_run[1]};
+    exps(neg_m, pf, sum);
+    if (__any(!(sum[0] <= kSumLimit) || !(sum[1] <= kSumLimit))) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int qt = 0; qt < 2; ++qt) {
+        float mx = s[0][qt][0];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-      mx = max_with_partner(mx * scale_log2);
-      const float m_new = mx > m_run ? mx : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (uint32_t dt = 0; dt < kDT; ++dt)
+          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kt][qt][e]);
+        mx = max_of_query(mx * scale_log2);
+        const float m_new = mx > m_run[qt] ? mx : m_run[qt];
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+        m_run[qt] = m_new;
+        neg_m[qt] = -m_new;
+        l_run[qt] *= alpha;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      sum = exps(-m_run, pf);
+        for (uint32_t dt = 0; dt < kDT; ++dt) o[dt][qt] *= alpha;
+      }
+      exps(neg_m, pf, sum);
     }
-    l_run += sum;
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int qt = 0; qt < 2; ++qt) l_run[qt] += sum[qt];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) pp[st][h] = pf[st][h];
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) pp[kk][qt] = pf[kk][qt];
   };
 
   auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi)
@@ -423,13 +428,11 @@ __device__ __forceinline__ void attention_block(
     // step overwrites.  The last block re-fetches its K tile: the DMA stays
     // unconditional, which keeps the compiler's wait counting exact.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // One path for every step (separate paths for the first block and for
-    // blocks past this wave's last made the compiler copy the output
-    // accumulators between register sets): the first step's output MFMAs
-    // add the zero probabilities pp starts with, and past the wave's last
-    // block every key is masked, so the softmax yields zeros and only the
-    // pending output update of the wave's last block counts.
-    float16_t s[2];
+    // One path for every step: the first step's output MFMAs add the zero
+    // probabilities pp starts with, and past the wave's last block every key
+    // is masked, so the softmax yields zeros and only the pending output
+    // update of the wave's last block counts.
+    float4_t s[4][2];
     cluster.template operator()<true>(s, lk, lv, nk, nv, kbi);
     softmax(s, kbi);
   };
@@ -444,9 +447,7 @@ __device__ __forceinline__ void attention_block(
   for (uint32_t i = 0; i < kTile / 16 / kThreads; ++i)
     *reinterpret_cast<u32x4*>(lds_v1 + (i * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
   // Both steps of a pair run unconditionally, so the loop body is one
-  // straight path (a skipped second step made the compiler merge the output
-  // accumulators from two paths with register copies); an odd last block
-  // runs after the loop.
+  // straight path; an odd last block runs after the loop.
   uint32_t kbi = 0;
   for (; kbi + 1 < nblocks; kbi += 2) {
     step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
@@ -457,29 +458,29 @@ __device__ __forceinline__ void attention_block(
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
-  // o[dt][r] = O^T[d = 32 dt + 8 (r/4) + 4 (lane/32) + r%4][qi], unnormalised.
-  const float l_total = sum_with_partner(l_run);
-  const float inv = 1.0f / l_total;
-  if (qi < query_rows) {
-    const uint64_t row = ((uint64_t)stream * query_rows + qi) * width;
+  // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
 #pragma unroll
-    for (uint32_t dt = 0; dt < kDT; ++dt)
+  for (int qt = 0; qt < 2; ++qt) {
+    const float inv = 1.0f / sum_of_query(l_run[qt]);
+    if (qi[qt] < query_rows) {
+      const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * width;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint32_t d = dt * 32 + 8 * g + 4 * (lane / 32);
+      for (uint32_t dt = 0; dt < kDT; ++dt) {
+        const uint32_t d = dt * 16 + 4 * g4;
         if (d >= width) continue;  // padding (width is a multiple of 8)
         if constexpr (OutF16) {
           half4_t hv;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][4 * g + e] * inv);
+          for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][qt][e] * inv);
           *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
         } else {
           float4_t fv;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) fv[e] = o[dt][4 * g + e] * inv;
+          for (int e = 0; e < 4; ++e) fv[e] = o[dt][qt][e] * inv;
           *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
         }
       }
+    }
   }
 }
 
