@@ -43,8 +43,10 @@
 //     one base), so the cluster's LDS reads take immediate offsets only;
 //   * causal: key blocks past the workgroup's last query are never loaded, a
 //     wave skips blocks past its own last query.
-//   * causal: one workgroup runs query blocks n - 1 - i and then i of one
-//     stream, so every workgroup has the same number of key steps;
+//   * a workgroup runs two query blocks of one stream back to back (causal:
+//     n - 1 - i and then i, so every workgroup has the same number of key
+//     steps); the first block's last step prefetches the second's first K
+//     tile and Q fragments;
 //     workgroups are remapped so each XCD (round-robin dispatch over 8) runs
 //     whole streams, sharing K and V in its L2.
 #include "../../include/ipus.h"
@@ -60,6 +62,7 @@ constexpr int kThreads = 256;
 constexpr int kQueriesPerWave = 32;
 constexpr int kQueriesPerBlock = 128;
 constexpr int kKeysPerBlock = 64;
+constexpr uint32_t kBlocksPerGroup = 2;  // query blocks per workgroup, run back to back
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
 constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
@@ -127,12 +130,51 @@ __device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes, uint32_t width
   return chunk * 8 < width ? row * row_bytes + chunk * 16 : kPadOffset;
 }
 
+// Key blocks of query block qb: causal blocks stop at the block's last query.
+template <bool Causal>
+__device__ __forceinline__ uint32_t key_blocks(uint32_t qb, uint32_t query_rows, uint32_t key_rows) {
+  uint32_t key_end = key_rows;
+  if (Causal) {
+    const uint32_t q0 = qb * kQueriesPerBlock;
+    const uint32_t last_q = q0 + kQueriesPerBlock < query_rows ? q0 + kQueriesPerBlock : query_rows;
+    key_end = last_q < key_rows ? last_q : key_rows;
+  }
+  return (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
+}
+
+// The wave's Q fragments for query block qb (second MFMA operand of the
+// scores): tile qt, k step ks holds Q[query][32 ks + 8 (l / 16) .. +7] of
+// query qb * 128 + 32 wave + 16 qt + l % 16 (clamped to the last row;
+// padding columns are 0).
+template <int D>
+__device__ __forceinline__ void load_q(half8_t (&qf)[2][D / 32], const uint16_t* __restrict__ query,
+                                       uint32_t stream, uint32_t qb, uint32_t query_rows,
+                                       uint32_t width, uint32_t q_heads) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t r16 = lane % 16, g4 = lane / 16;
+  const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t wq0 = qb * kQueriesPerBlock + wave_s * kQueriesPerWave;
+  const uint32_t q_pitch = q_heads * width;
+  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * width;
+#pragma unroll
+  for (uint32_t qt = 0; qt < 2; ++qt) {
+    uint32_t q = wq0 + 16 * qt + r16;
+    q = q < query_rows ? q : query_rows - 1;
+#pragma unroll
+    for (uint32_t ks = 0; ks < D / 32; ++ks) {
+      const uint32_t d0 = ks * 32 + g4 * 8;
+      qf[qt][ks] = __builtin_bit_cast(
+          half8_t, d0 < width ? load16(Q + (uint64_t)q * q_pitch + d0) : u32x4{0, 0, 0, 0});
+    }
+  }
+}
+
 template <int D, bool Causal, bool OutF16>
 __device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
     uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
-    uint32_t v_heads) {
+    uint32_t v_heads, half8_t (&qf)[2][D / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
   constexpr uint32_t kKS = D / 32;  // k steps (32 columns) of the score MFMAs
   constexpr uint32_t kDT = D / 16;  // output d tiles (16 columns)
   constexpr uint32_t kPairs = 4 * kKS;  // score MFMA pairs (query tiles 0, 1) per key block
@@ -156,9 +198,7 @@ __device__ __forceinline__ void attention_block(
   // Stream s of an operand with h heads is head s % h of matrix s / h of a
   // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
   // The tile width D is the stream width padded to 64 or 128.
-  const uint32_t q_pitch = q_heads * width;
   const uint32_t k_row_bytes = k_heads * width * 2u, v_row_bytes = v_heads * width * 2u;
-  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * width;
   const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_heads * width + (stream % k_heads) * width;
   const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * width + (stream % v_heads) * width;
   const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -168,12 +208,7 @@ __device__ __forceinline__ void attention_block(
   const uint32_t k_voff = kv_offset<D, true>(k_row_bytes, width);
   const uint32_t v_voff = kv_offset<D, false>(v_row_bytes, width);
 
-  uint32_t key_end = key_rows;
-  if (Causal) {
-    const uint32_t last_q = q0 + kQueriesPerBlock < query_rows ? q0 + kQueriesPerBlock : query_rows;
-    key_end = last_q < key_rows ? last_q : key_rows;  // keys <= last query
-  }
-  const uint32_t nblocks = (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
+  const uint32_t nblocks = key_blocks<Causal>(qb, query_rows, key_rows);
   const uint32_t k_block_bytes = kKeysPerBlock * k_row_bytes;
   const uint32_t v_block_bytes = kKeysPerBlock * v_row_bytes;
   // Blocks this wave computes scores for (causal: keys <= its last query).
@@ -182,22 +217,6 @@ __device__ __forceinline__ void attention_block(
   if (Causal) {
     const uint32_t lim = (wq0 + kQueriesPerWave - 1) / kKeysPerBlock + 1;
     nproc = lim < nproc ? lim : nproc;
-  }
-
-  // The wave's 32 queries are two tiles of 16 (qt); lane l serves query
-  // wq0 + 16 qt + l % 16 of each.  Q fragments (second MFMA operand of the
-  // scores) for tile qt, k step ks: Q[query][32 ks + 8 (l / 16) .. +7].
-  half8_t qf[2][kKS];
-#pragma unroll
-  for (uint32_t qt = 0; qt < 2; ++qt) {
-    uint32_t q = wq0 + 16 * qt + r16;
-    q = q < query_rows ? q : query_rows - 1;
-#pragma unroll
-    for (uint32_t ks = 0; ks < kKS; ++ks) {
-      const uint32_t d0 = ks * 32 + g4 * 8;  // padding columns are 0
-      qf[qt][ks] = __builtin_bit_cast(
-          half8_t, d0 < width ? load16(Q + (uint64_t)q * q_pitch + d0) : u32x4{0, 0, 0, 0});
-    }
   }
 
   float4_t o[kDT][2];
@@ -275,7 +294,7 @@ __device__ __forceinline__ void attention_block(
   // d tile p % kDT), each over query tiles 0 and 1 with one fragment read.
   auto cluster = [&]<bool WithPv>(float4_t (*s)[2], const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
                                    uint8_t* nv, uint32_t kbi) __attribute__((always_inline)) {
-    const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : kbi;
+    const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : (chain ? 0u : kbi);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -442,7 +461,8 @@ __device__ __forceinline__ void attention_block(
   // is zeroed here (whatever an earlier kernel left in LDS may hold
   // non-finite fp16 patterns; 0 * inf is NaN).
 #pragma unroll
-  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i) dma_k(i, lds_k0, 0);
+  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
+    if (!k0_loaded) dma_k(i, lds_k0, 0);
 #pragma unroll
   for (uint32_t i = 0; i < kTile / 16 / kThreads; ++i)
     *reinterpret_cast<u32x4*>(lds_v1 + (i * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
@@ -456,6 +476,7 @@ __device__ __forceinline__ void attention_block(
   if (kbi < nblocks) step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
   // V of the last block (and every DMA) has landed after this barrier.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (chain) load_q<D>(qf, query, stream, next_qb, query_rows, width, q_heads);
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
   // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
@@ -484,9 +505,13 @@ __device__ __forceinline__ void attention_block(
   }
 }
 
-// One workgroup per query block (non-causal), or per pair of query blocks
-// i and n - 1 - i of one stream (causal: the pair's key steps add up to the
-// same count for every workgroup).  Workgroups are remapped so each XCD
+// One workgroup per pair of query blocks of one stream: 2 i and 2 i + 1
+// (non-causal), or n - 1 - i and i (causal: the pair's key steps add up to
+// the same count for every workgroup).  When the first block's key block
+// count is even, its last step fetches the second block's first K tile and
+// its epilogue the second block's Q fragments, so the second block starts
+// without a load latency (and without the burst of loads that workgroups
+// starting together would issue).  Workgroups are remapped so each XCD
 // (round-robin dispatch over 8) runs whole streams, sharing K and V in its L2.
 template <int D, bool Causal, bool OutF16>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
@@ -494,20 +519,34 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
     uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
   const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const uint32_t per_stream = Causal ? (qblocks + 1) / 2 : qblocks;
+  const uint32_t per_stream = (qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup;
   const uint32_t total = per_stream * streams;
   uint32_t pid = blockIdx.x;
   if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;  // XCD-contiguous
   const uint32_t stream = pid / per_stream, i = pid % per_stream;
-  // Causal: the heavy block first, then its mirror (none for the middle
-  // block of an odd count).
-  const uint32_t reps = Causal && i != qblocks - 1 - i ? 2 : 1;
+  // Block order within a stream: causal n - 1, 0, n - 2, 1, ... (the heavy
+  // block, then its mirror: each pair has the same key steps), otherwise
+  // 0, 1, 2, ...; this workgroup runs the pair at positions 2 i, 2 i + 1.
+  auto qb_at = [&](uint32_t pos) {
+    return Causal ? (pos % 2 == 0 ? qblocks - 1 - pos / 2 : pos / 2) : pos;
+  };
+  const uint32_t pos0 = i * kBlocksPerGroup;
+  const uint32_t reps = qblocks - pos0 < kBlocksPerGroup ? qblocks - pos0 : kBlocksPerGroup;
+  half8_t qf[2][D / 32];
+  load_q<D>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
+  bool loaded = false;  // this block's first K tile and Q fragments were fetched by the last one
   for (uint32_t rep = 0; rep < reps; ++rep) {
     // Every wave is done with the LDS stages before the next block's DMA.
-    if (rep > 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const uint32_t qb = Causal ? (rep == 0 ? qblocks - 1 - i : i) : i;
+    if (rep > 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint32_t qb = qb_at(pos0 + rep);
+    // A block with an even key block count ends in stage 1, so its last
+    // step can fetch the next block's first K tile into stage 0.
+    const bool chain = rep + 1 < reps && key_blocks<Causal>(qb, query_rows, key_rows) % 2 == 0;
+    if (rep > 0 && !loaded) load_q<D>(qf, query, stream, qb, query_rows, width, q_heads);
     attention_block<D, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
-                                       width, scale_log2, q_heads, k_heads, v_heads);
+                                       width, scale_log2, q_heads, k_heads, v_heads, qf, loaded,
+                                       chain, qb_at(pos0 + rep + 1));
+    loaded = chain;
   }
 }
 
@@ -572,7 +611,7 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
 template <int D, bool Causal, bool OutF16>
 int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   const uint32_t qblocks = (a.query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const uint64_t blocks = (uint64_t)(Causal ? (qblocks + 1) / 2 : qblocks) * a.streams;
+  const uint64_t blocks = (uint64_t)((qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup) * a.streams;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
   hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
