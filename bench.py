@@ -584,8 +584,9 @@ def summarize_counters(directory: str, skip: int, command: str, xcds: int = 8,
     --pmc pass holding SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE (and any
     other counters, reported as medians).  GRBM_GUI_ACTIVE is summed over the
     XCDs, so the shader clock is GRBM_GUI_ACTIVE / xcds / duration;
-    SQ_VALU_MFMA_BUSY_CYCLES counts 32 cycles per v_mfma_f32_32x32x16_f16
-    over all SIMDs, so the utilisation is that over shader cycles x SIMDs."""
+    SQ_VALU_MFMA_BUSY_CYCLES counts the matrix pipes' busy cycles over all
+    SIMDs (16 per v_mfma_f32_16x16x32_f16, 32 per v_mfma_f32_32x32x16_f16),
+    so the utilisation is that over shader cycles x SIMDs."""
     prof = _profiling()
     report = prof.from_rocprof(counter_csv=directory)
     keep = _timed_phases(report, skip)
