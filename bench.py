@@ -20,7 +20,8 @@ the same run).  results{} adds the median of 5 such regions and the launches
 timed one by one with an event before each: an event between two launches
 makes the second wait for the first to drain, which serializes them (~9%
 slower at 8192^3).  The other legs time 5 regions of back-to-back launches
-between two events each and report the median region.
+between two events each and report the median region; the MFMA legs (fp32
+GEMM, attention, MLP graph) run settle launches first as the headline does.
 Bandwidth kernels rotate 3 buffer sets (768 MiB > the 256 MiB MALL).  One
 JSON line on stdout.
 
@@ -70,14 +71,19 @@ class Timing(dict):
 
 
 def timed(ctx, fn, steps: int, warmup: int, per_launch: bool = False,
-          repeats: int = 5) -> Timing:
+          repeats: int = 5, settle: int = 0) -> Timing:
     """`warmup` untimed calls of `fn` (which enqueues on the stream) and a
     synchronisation, then timed calls on HIP events.  per_launch: `steps`
     calls with an event before each and after the last, so each call has its
     own duration (the headline: exactly K timed steps).  Otherwise `repeats`
     regions of `steps` back-to-back calls between two events each, so short
     kernels carry no per-launch event gaps; the median is over the regions'
-    per-call means."""
+    per-call means.  `settle` untimed calls and a synchronisation come first
+    (MFMA legs: the board's power controller needs ~30-50 ms of load after
+    idle to settle; see SETTLE_LAUNCHES)."""
+    for _ in range(settle):
+        fn(0)
+    ctx.sync()
     for _ in range(warmup):
         fn(0)
     ctx.sync()
@@ -129,10 +135,7 @@ def bench_gemm_f16(ipus, ctx, n, steps, warmup, per_launch=False, repeats=5, set
     b = ctx.upload(ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM))
     c = ctx.alloc(n * n * 2)
     fn = lambda i: ctx.launch("ipu_stack_gemm_f16", c, [a, b], gemm_scalars(n))  # noqa: E731
-    for i in range(settle):
-        fn(i)
-    ctx.sync()
-    ms = timed(ctx, fn, steps, warmup, per_launch=per_launch, repeats=repeats)
+    ms = timed(ctx, fn, steps, warmup, per_launch=per_launch, repeats=repeats, settle=settle)
     for x in (a, b, c):
         x.free()
     return ms
@@ -159,18 +162,18 @@ def bench_gemm_f16_graph(ipus, ctx, n, steps, warmup, copies=64):
                   min_ms=t["min_ms"] / copies, max_ms=t["max_ms"] / copies, launches=t["launches"])
 
 
-def bench_gemm_f32(ipus, ctx, n, steps, warmup):
+def bench_gemm_f32(ipus, ctx, n, steps, warmup, settle=0):
     a = ctx.upload(ipus.synth_f32(n * n, 4096, 1, ipus.NORMAL))
     b = ctx.upload(ipus.synth_f32(n * n, 4096, 2, ipus.NORMAL))
     c = ctx.alloc(n * n * 4)
     ms = timed(ctx, lambda i: ctx.launch("ipu_stack_gemm_f32", c, [a, b], gemm_scalars(n)),
-               steps, warmup)
+               steps, warmup, settle=settle)
     for x in (a, b, c):
         x.free()
     return ms
 
 
-def bench_attention(ipus, ctx, s, causal, steps, warmup, streams=128, d=128):
+def bench_attention(ipus, ctx, s, causal, steps, warmup, streams=128, d=128, settle=0):
     n = streams * s * d
     q = ctx.upload(ipus.synth_f16(n, 5, 1, ipus.NORMAL))
     k = ctx.upload(ipus.synth_f16(n, 5, 2, ipus.NORMAL))
@@ -178,7 +181,7 @@ def bench_attention(ipus, ctx, s, causal, steps, warmup, streams=128, d=128):
     o = ctx.alloc(n * 4)
     sc = [streams, s, s, d, d, 0, int(causal), 0]
     ms = timed(ctx, lambda i: ctx.launch("ipu_stack_flash_attention_online_f16", o, [q, k, v], sc),
-               steps, warmup)
+               steps, warmup, settle=settle)
     for x in (q, k, v, o):
         x.free()
     return ms
@@ -248,7 +251,7 @@ def bench_gelu(ipus, ctx, steps, warmup, rows=4096, cols=16384, sets=3):
     return ms
 
 
-def bench_mlp_graph(ipus, ctx, steps, warmup):
+def bench_mlp_graph(ipus, ctx, steps, warmup, settle=0):
     """configs[3] through ComputeGraph + build_package + session."""
     g = ipus.ComputeGraph()
     xin = g.host_input("input", [4096, 4096])
@@ -260,7 +263,7 @@ def bench_mlp_graph(ipus, ctx, steps, warmup):
     sess.write("input", ipus.synth_f16(4096 * 4096, 9, 1, ipus.NORMAL).reshape(4096, 4096))
     sess.write("w1", ipus.synth_f16(4096 * 16384, 9, 2, ipus.NORMAL, 0.02).reshape(4096, 16384))
     sess.write("w2", ipus.synth_f16(16384 * 4096, 9, 3, ipus.NORMAL, 0.02).reshape(16384, 4096))
-    ms = timed(ctx, lambda i: sess.run(), steps, warmup)
+    ms = timed(ctx, lambda i: sess.run(), steps, warmup, settle=settle)
     sess.close()
     return ms
 
@@ -653,6 +656,9 @@ def device_name(info: dict) -> str:
 # while the board's power controller settles; from the fourth region of 20 on
 # they hold 1,500-1,550 for as long as measured (1.2 s).
 SETTLE_LAUNCHES = 60
+# The same for the attention legs (0.27-0.57 ms a launch; from idle the
+# causal S4096 rate climbs from ~900 to ~1,040 TFLOP/s over ~60 launches).
+ATTENTION_SETTLE_LAUNCHES = 200
 
 LEGS = ("mfma_calibration", "gemm_f32_4096", "attention_causal_s4096",
         "attention_noncausal_s2048", "memory_chain", "amp_layouts", "gelu_4096x16384",
@@ -675,14 +681,14 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
         results["mfma_calibration"] = cal
         log(f"mfma calibration: {cal}")
     if want("gemm_f32_4096"):
-        t = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2)
+        t = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2, settle=SETTLE_LAUNCHES)
         results["gemm_f32_4096"] = leg_entry(t, 2.0 * 4096 ** 3, "tflops", PEAK_FP32_TFLOPS)
         log(f"gemm_f32 4096^3: {results['gemm_f32_4096']}")
     for causal, s in ((True, 4096), (False, 2048)):
         key = f"attention_{'causal' if causal else 'noncausal'}_s{s}"
         if not want(key):
             continue
-        t = bench_attention(ipus, ctx, s, causal, sub_steps, 2)
+        t = bench_attention(ipus, ctx, s, causal, sub_steps, 2, settle=ATTENTION_SETTLE_LAUNCHES)
         fl = 4.0 * 128 * 128 * (s * (s + 1) / 2 if causal else s * s)
         results[key] = leg_entry(t, fl, "tflops", PEAK_FP16_TFLOPS)
         log(f"{key}: {results[key]}")
@@ -702,7 +708,7 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
         results["gelu_4096x16384"] = leg_entry(t, 2 * 4096 * 16384 * 2, "gbps", PEAK_HBM_GBPS)
         log(f"gelu: {results['gelu_4096x16384']}")
     if want("mlp_graph"):
-        t = bench_mlp_graph(ipus, ctx, args.steps, 3)
+        t = bench_mlp_graph(ipus, ctx, args.steps, 3, settle=SETTLE_LAUNCHES)
         results["mlp_graph"] = leg_entry(t, 2 * 2.0 * 4096 * 4096 * 16384, "tflops",
                                          PEAK_FP16_TFLOPS)
         log(f"mlp graph: {results['mlp_graph']}")
