@@ -456,10 +456,13 @@ __device__ __forceinline__ void attention_block(
     softmax(s, kbi);
   };
 
-  // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j).  The first
-  // step's output MFMAs multiply zero probabilities with V stage 1, which
-  // is zeroed here (whatever an earlier kernel left in LDS may hold
-  // non-finite fp16 patterns; 0 * inf is NaN).
+  // Block j lives in stage j % 2 (lds_k0 / lds_v0 for even j); K(0) is
+  // fetched here unless the previous block's last step already did.  The
+  // first step's output MFMAs multiply zero probabilities with V stage 1,
+  // which is zeroed here (whatever an earlier kernel or block left in LDS
+  // may hold non-finite fp16 patterns; 0 * inf is NaN).  With a chained
+  // next block, its Q fragments are loaded once this block's last scores
+  // are done with them.
 #pragma unroll
   for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
     if (!k0_loaded) dma_k(i, lds_k0, 0);
