@@ -74,12 +74,12 @@ def timed(ctx, fn, steps: int, warmup: int, per_launch: bool = False,
     """`warmup` untimed calls of `fn` (which enqueues on the stream) and a
     synchronisation, then timed calls on HIP events.  per_launch: `steps`
     calls with an event before each and after the last, so each call has its
-    own duration (the headline: exactly K timed steps).  Otherwise `repeats`
-    regions of `steps` back-to-back calls between two events each, so short
-    kernels carry no per-launch event gaps; the median is over the regions'
-    per-call means.  `settle` untimed calls and a synchronisation come first
-    (MFMA legs: the board's power controller needs ~30-50 ms of load after
-    idle to settle; see SETTLE_LAUNCHES)."""
+    own duration.  Otherwise `repeats` regions of `steps` back-to-back calls
+    between two events each (the headline: one region of exactly K steps),
+    so short kernels carry no per-launch event gaps; the median is over the
+    regions' per-call means.  `settle` untimed calls and a synchronisation
+    come first (MFMA legs: the board's power controller needs ~30-50 ms of
+    load after idle to settle; see SETTLE_LAUNCHES)."""
     for _ in range(settle):
         fn(0)
     ctx.sync()
