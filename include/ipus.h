@@ -49,6 +49,11 @@ extern "C" {
 #define IPUS_ERROR_BUILD (-7)              /* PackageBuildError (package.rs:48-78) */
 #define IPUS_ERROR_NO_DEVICE (-8)
 #define IPUS_ERROR_OUT_OF_MEMORY (-9)
+/* A reference symbol that names an IPU tile codelet with no per-tile GPU
+ * counterpart (the tile GEMM codelets, the staged-attention codelets): the
+ * caller translates the whole operator to one launch instead.  The message
+ * names the replacement symbol. */
+#define IPUS_ERROR_TRANSLATED (-10)
 #define IPUS_ERROR_HIP_BASE (-1000)        /* IPUS_ERROR_HIP_BASE - hipError_t */
 
 /* Message of the calling thread's most recent failure ("" if none). */
@@ -60,7 +65,9 @@ const char *ipus_version(void);
 typedef struct ipus_context ipus_context;
 
 typedef struct ipus_device_info {
-  char name[64];          /* e.g. "AMD Instinct MI355X" */
+  char name[64];          /* e.g. "AMD Instinct MI355X"; where the runtime
+                             reports none, the driver's sysfs product_name
+                             of the device's PCI function */
   char arch[32];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
   int compute_units;
   int clock_khz;
@@ -123,6 +130,17 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        ipu_stack_gemm_f16 followed by ipu_stack_gelu_tanh_approx_f16).  No
  *        reference symbol: build_package fuses a Gemm whose result feeds only
  *        one Gelu (graph.rs:315-331) into this launch.
+ *   ipu_stack_gemm_f16_accumulate      out f16 [B,M,N]; left, right, addend
+ *        f16; the ipu_stack_gemm_f16 scalars, then addend_batch_stride,
+ *        addend_row_stride (elements; 0 broadcasts the addend over batches /
+ *        rows): out = addend + A.B with the product rounded to fp16 first
+ *        and the sum formed like ipu_stack_add_f16 (fp32 add, one rounding),
+ *        so it is bit-identical to ipu_stack_gemm_f16 followed by that Add.
+ *        The addend may be the output itself (the reference's accumulate
+ *        mode, C += A.B: device/gemm_f16_amp.S:43-52, 290-363, used after
+ *        the first K block by crates/ipu-codegen/src/low.rs:3483-3486), but
+ *        the output must not overlap A or B.  build_package fuses a Gemm
+ *        whose result only feeds an Add into this launch.
  *   ipu_stack_gemm_f16_split           out fp32 partials
  *        float[splits][batches][rows][columns]; inputs as ipu_stack_gemm_f16;
  *        scalars as ipu_stack_gemm_f16 plus splits: split z sums k in
@@ -137,6 +155,10 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        splits, element_count (a multiple of 8), gelu (0/1): the sum over
  *        splits in order, rounded to fp16 once (GELU of that value when
  *        gelu = 1, as in ipu_stack_gemm_f16_gelu).
+ *   ipu_stack_reduce_splits_accumulate_f16  out f16; partials, addend f16;
+ *        splits, batches, rows, columns, addend_batch_stride,
+ *        addend_row_stride: the split sum rounded to fp16, plus the addend
+ *        as in ipu_stack_gemm_f16_accumulate (columns a multiple of 8).
  *   ipu_stack_gemm_f32                 as above in fp32
  *        (device/gemm_f32_64_amp.S:125-385).
  *   ipu_stack_flash_attention_online_f16  out (f32 or f16); query, key,
@@ -173,8 +195,47 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        [rows, columns]; rows, columns, source_order (3 row-major,
  *        2 block-major), row_block, column_block.  ReductionSum over the
  *        columns with fp32 accumulation (operator.rs:307-347).
- *   ipu_stack_fill_zero                out; no inputs; byte_count
- *        (FillZero, kernel.rs:1231-1236).
+ *   ipu_stack_fill_zero                out; no inputs; byte_count.  The
+ *        plan's own FillZero step (arena values, fp32 partials); no reference
+ *        symbol.
+ *   ipu_stack_fill_zero_u64            out; no inputs; words_per_worker,
+ *        remainder_workers: the reference's FillZero step as
+ *        materialize_kernel_run emits it (FILL_ZERO_U64_SYMBOL,
+ *        crates/ipu-target/src/emit.rs:38; scalars kernel.rs:1223-1229,
+ *        1175-1176): zeroes 8 * (6 * words_per_worker + remainder_workers)
+ *        bytes; remainder_workers must be < 6.
+ *
+ * Reference per-shape symbols.  The reference links one specialization per
+ * operand shape and names it by that shape (KernelBuildPlan::from_program,
+ * kernel.rs:321-328, 374-379, 506-515).  ipus_kernel_abi, ipus_launch and
+ * ipus_validate_kernel_run accept those names; the suffix fixes the shape of
+ * one launch of the generic kernel:
+ *   ipu_stack_rearrange_row_major_to_amp_f16_o{T}_r{LR}_p{PR}_c{LC}_p{PC}
+ *        out; source row-major; the reference's scalars logical_rows,
+ *        physical_rows, target_order (= T), logical_columns,
+ *        physical_columns (kernel.rs:1351-1361), one matrix.  The scalars'
+ *        physical extents must equal the suffix, and the logical ones too
+ *        unless the suffix holds 0 there (rearrangement_specialization,
+ *        kernel.rs:1122-1146).  T = 2 is block-major {64, 16}, the one block
+ *        shape the reference plans for this conversion (layout.rs:356-361).
+ *        Replaces rearrange_amp_left_f16.S, rearrange_block_major_f16.S,
+ *        rearrange_transposed_right_f16.S and rearrange_f16.cpp.
+ *   ipu_stack_unpack_amp_to_row_major_f16_o{S}_r{LR}_p{PR}_c{LC}_p{PC}
+ *        out row-major; source AMP-Output (S = 0) or AMP-TransposedLeft
+ *        (S = 1); scalars matrices, logical_rows, physical_rows,
+ *        logical_columns, physical_columns (kernel.rs:1327-1336), extents
+ *        equal to the suffix (device/unpack_amp_f16.cpp:6-40).
+ *   ipu_stack_flash_attention_online_f16_m{B}_q{Q}_k{K}_d{D}_v{V}_{scale:08x}
+ *        out f32; query, key, value f16 row-major; no scalars
+ *        (AttentionKernelShape, kernel.rs:121-129, 986-1040): non-causal,
+ *        scale = the f32 with those bits.
+ * Reference symbols that are not forwarded return IPUS_ERROR_TRANSLATED
+ * (the tile GEMM codelets ipu_stack_gemm_{f16,f32}_{init,accumulate}_...,
+ * kernel.rs:185-193, and the staged-attention codelets
+ * ipu_stack_attention_{softmax,merge}_..., kernel.rs:546-640) or
+ * IPUS_ERROR_UNAVAILABLE (symbols the reference itself marks Required:
+ * fp8 GEMM and casts, ipu_stack_unsupported_*).
+ *
  *   ipu_stack_cast_f32_f16, ipu_stack_cast_f16_f32   out; input;
  *        element_count (Cast, kernel.rs:1313-1318).
  *   ipu_stack_add_f16, ipu_stack_add_f32   out; left, right; element_count,
@@ -208,6 +269,15 @@ typedef struct ipus_kernel_abi_info {
 int ipus_kernel_count(int *count);
 int ipus_kernel_abi_at(int index, ipus_kernel_abi_info *info);
 int ipus_kernel_abi(const char *symbol, ipus_kernel_abi_info *info);
+
+/* validate_kernel_run (kernel.rs:1384-1435) without a device: the symbol
+ * resolves (including the reference per-shape names above), pointer arity
+ * and scalar count match its ABI, and the scalars meet its constraints
+ * (even GELU count, reduce partials and count, FillZero remainder, per-shape
+ * suffix agreement).  Returns 0 or the status ipus_launch would return for
+ * the same call before touching the device. */
+int ipus_validate_kernel_run(const char *symbol, int input_count, const uint32_t *scalars,
+                             int scalar_count);
 
 /* One ComputeStep{symbol, output_address, input_addresses, arguments}:
  * validates pointer arity and scalar constraints (validate_kernel_run,

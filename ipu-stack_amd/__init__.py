@@ -48,6 +48,7 @@ ERROR_GRAPH = -6
 ERROR_BUILD = -7
 ERROR_NO_DEVICE = -8
 ERROR_OUT_OF_MEMORY = -9
+ERROR_TRANSLATED = -10
 ERROR_HIP_BASE = -1000
 
 MAX_RANK = 8
@@ -172,6 +173,8 @@ _SIGNATURES = {
     "ipus_kernel_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
     "ipus_kernel_abi_at": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_KernelAbiInfo)]),
     "ipus_kernel_abi": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_KernelAbiInfo)]),
+    "ipus_validate_kernel_run": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, _U32P,
+                                                ctypes.c_int]),
     "ipus_launch": (
         ctypes.c_int,
         [_P, ctypes.c_char_p, _P, ctypes.POINTER(_P), ctypes.c_int, _U32P, ctypes.c_int],
@@ -282,7 +285,7 @@ def _check(status: int, kind: type = IpusError) -> None:
         elif status == ERROR_BUILD:
             kind = PackageBuildError
         elif status in (ERROR_POINTER_ARITY, ERROR_UNAVAILABLE, ERROR_UNSUPPORTED_COUNT,
-                        ERROR_UNKNOWN_SYMBOL):
+                        ERROR_UNKNOWN_SYMBOL, ERROR_TRANSLATED):
             kind = KernelAbiError
         raise kind(status, last_error())
 
@@ -331,6 +334,15 @@ def kernel_abi(symbol: str) -> KernelAbi:
     info = _KernelAbiInfo()
     _check(_lib().ipus_kernel_abi(symbol.encode(), ctypes.byref(info)))
     return _abi_from(info)
+
+
+def validate_kernel_run(symbol: str, input_count: int, scalars: Sequence[int]) -> None:
+    """validate_kernel_run (crates/ipu-codegen/src/kernel.rs:1384-1435) on
+    the host: raises KernelAbiError (or IpusError) with the status that
+    ``Context.launch`` would return for the same step, before any device
+    work."""
+    arr, n = _u32_array(scalars)
+    _check(_lib().ipus_validate_kernel_run(symbol.encode(), int(input_count), arr, n))
 
 
 # ---------------------------------------------------------------------------

@@ -982,6 +982,106 @@ void fuse_gemm_gelu(ipus_package& pkg) {
   pkg.steps = std::move(steps);
 }
 
+// An fp16 Gemm whose whole result is read only by the Add that follows it
+// (the residual x + x . W of graph.rs:12-33 and of Repeat bodies, or a bias)
+// becomes one ipu_stack_gemm_f16_accumulate launch: the epilogue rounds the
+// product to fp16 and adds the other operand like the Add kernel does, so
+// the result is bit-identical, and the product's write and read disappear.
+// The other operand must broadcast only as whole rows or whole matrices
+// (column stride 1; batch axes collapsing to one stride).  A split-K GEMM
+// fuses into its reduction (ipu_stack_reduce_splits_accumulate_f16).
+void fuse_gemm_add(ipus_package& pkg) {
+  std::vector<int> reads(pkg.slots.size(), 0), writes(pkg.slots.size(), 0);
+  for (const Step& s : pkg.steps) {
+    ++writes[(size_t)s.out.slot];
+    for (const Operand& o : s.ins) ++reads[(size_t)o.slot];
+  }
+  std::vector<Step> steps;
+  for (size_t i = 0; i < pkg.steps.size(); ++i) {
+    const Step& s = pkg.steps[i];
+    const bool gemm = s.symbol == "ipu_stack_gemm_f16";
+    const bool split_reduce = s.symbol == "ipu_stack_reduce_splits_f16" && s.scalars[2] == 0;
+    if (i + 1 >= pkg.steps.size() || !(gemm || split_reduce) || s.out.byte_offset != 0) {
+      steps.push_back(s);
+      continue;
+    }
+    const Step& n = pkg.steps[i + 1];
+    const int mid = s.out.slot;
+    const Slot& ms = pkg.slots[(size_t)mid];
+    if (n.symbol != "ipu_stack_add_broadcast_f16" || n.ins.size() != 2 || ms.external ||
+        writes[(size_t)mid] != 1 || reads[(size_t)mid] != 1 ||
+        (n.ins[0].slot == mid) == (n.ins[1].slot == mid)) {
+      steps.push_back(s);
+      continue;
+    }
+    // add_broadcast scalars: rank, shape[6], left strides[6], right strides[6]
+    const int which = n.ins[0].slot == mid ? 0 : 1;
+    const Operand product = n.ins[(size_t)which], addend = n.ins[(size_t)(1 - which)];
+    const uint32_t rank = n.scalars[0];
+    auto shape = [&](uint32_t ax) { return n.scalars[1 + ax]; };
+    auto stride = [&](int op, uint32_t ax) { return n.scalars[7 + 6 * (size_t)op + ax]; };
+    bool ok = rank >= 2 && product.byte_offset == 0;
+    // The product covers the Add's whole output densely (strides of size-1
+    // axes are 0 in the lowering).
+    uint64_t dense = 1;
+    for (int ax = (int)rank - 1; ok && ax >= 0; --ax) {
+      const uint32_t want = shape((uint32_t)ax) == 1 ? 0 : (uint32_t)dense;
+      ok = stride(which, (uint32_t)ax) == want;
+      dense *= shape((uint32_t)ax);
+    }
+    if (!ok || dense != elements(ms.storage.shape)) {
+      steps.push_back(s);
+      continue;
+    }
+    const uint32_t M = shape(rank - 2), N = shape(rank - 1), other = (uint32_t)(1 - which);
+    ok = N == 1 || stride(other, rank - 1) == 1;
+    const uint32_t row_stride = M == 1 ? 0 : stride(other, rank - 2);
+    // Batch axes collapse to one stride: the innermost non-1 axis sets it,
+    // each outer one must be that stride times the batches inside it.
+    int64_t batch_stride = -1;
+    uint64_t inner = 1;
+    for (int ax = (int)rank - 3; ok && ax >= 0; --ax) {
+      const uint32_t extent = shape((uint32_t)ax);
+      if (extent != 1) {
+        const uint64_t st = stride(other, (uint32_t)ax);
+        if (batch_stride < 0) {
+          ok = st % inner == 0;
+          batch_stride = (int64_t)(st / inner);
+        } else {
+          ok = st == (uint64_t)batch_stride * inner;
+        }
+      }
+      inner *= extent;
+    }
+    const uint64_t batches = dense / ((uint64_t)M * N);
+    if (batch_stride < 0) batch_stride = 0;
+    if (ok && gemm) ok = s.scalars[0] == batches && s.scalars[1] == M && s.scalars[2] == N;
+    // The split reduction loads the addend as 16-byte chunks.
+    if (ok && split_reduce)
+      ok = N % 8 == 0 && row_stride % 8 == 0 && batch_stride % 8 == 0 &&
+           addend.byte_offset % 16 == 0 && fits_u32(batches);
+    if (!ok || !fits_u32((uint64_t)batch_stride)) {
+      steps.push_back(s);
+      continue;
+    }
+    Step f = s;
+    if (gemm) {
+      f.symbol = "ipu_stack_gemm_f16_accumulate";
+      f.ins.push_back(addend);
+      f.scalars.push_back((uint32_t)batch_stride);
+      f.scalars.push_back(row_stride);
+    } else {
+      f.symbol = "ipu_stack_reduce_splits_accumulate_f16";
+      f.ins.push_back(addend);
+      f.scalars = {s.scalars[0], (uint32_t)batches, M, N, (uint32_t)batch_stride, row_stride};
+    }
+    f.out = n.out;
+    steps.push_back(std::move(f));
+    ++i;
+  }
+  pkg.steps = std::move(steps);
+}
+
 bool is_attention(const std::string& symbol) {
   return symbol == "ipu_stack_flash_attention_online_f16" ||
          symbol == "ipu_stack_flash_attention_heads_f16";
@@ -1173,6 +1273,7 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
   // Precision map (CompiledPackage::precisions) over every value bound to a slot.
   for (const auto& kv : b.env) pkg->precisions[kv.first] = pkg->slots[(size_t)kv.second].storage.precision;
   fuse_gemm_gelu(*pkg);
+  fuse_gemm_add(*pkg);
   elide_split_heads(*pkg);
   pkg->arena_bytes = place(*pkg);
   *out = pkg.release();

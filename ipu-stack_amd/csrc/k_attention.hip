@@ -64,8 +64,9 @@ constexpr int kQueriesPerBlock = 128;
 constexpr int kKeysPerBlock = 64;
 constexpr uint32_t kBlocksPerGroup = 2;  // query blocks per workgroup, run back to back
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleSlack = 8.0f;
-constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
+// A block whose probabilities, taken against the current reference point,
+// sum to at most 2^8 per lane is accepted without moving the reference.
+constexpr float kSumLimit = 256.0f;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, dword 3 of the descriptor
 
 typedef short short4_t __attribute__((vector_size(8)));

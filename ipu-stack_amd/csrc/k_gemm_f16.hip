@@ -163,14 +163,32 @@ __device__ __forceinline__ void issue_one(__amdgpu_buffer_rsrc_t rsrc, uint8_t* 
   dma16(rsrc, tile + inst * 1024, voff, soffset);
 }
 
-// fp16 result of one accumulator; with Gelu, GELU of that fp16 value (the
+// Epilogues: the plain fp16 product; GELU of it; or the sum of it and an
+// addend element (C += A . B, the reference's accumulate mode).
+enum Epilogue : int { kEpiPlain = 0, kEpiGelu = 1, kEpiAdd = 2 };
+
+// fp16 result of one accumulator; with GELU, GELU of that fp16 value (the
 // same number the separate GELU kernel would produce from the stored GEMM
-// output).
-template <bool Gelu>
+// output).  The add epilogue applies add_f16 to this value afterwards.
+template <int Epi>
 __device__ __forceinline__ half_t epilogue(float acc) {
   const half_t h = (half_t)acc;
-  if constexpr (Gelu) return (half_t)gelu_tanh((float)h);
+  if constexpr (Epi == kEpiGelu) return (half_t)gelu_tanh((float)h);
   return h;
+}
+
+// The fp16 Add kernel's arithmetic (k_memory.hip add_kernel): both operands
+// widened to fp32, summed, rounded once to fp16, so a fused accumulate is
+// bit-identical to a GEMM followed by an Add.
+__device__ __forceinline__ half_t add_f16(half_t product, half_t addend) {
+  return (half_t)((float)addend + (float)product);
+}
+__device__ __forceinline__ u32x4 add_f16x8(u32x4 product, u32x4 addend) {
+  const half8_t p = __builtin_bit_cast(half8_t, product), a = __builtin_bit_cast(half8_t, addend);
+  half8_t r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = add_f16(p[e], a[e]);
+  return __builtin_bit_cast(u32x4, r);
 }
 
 // Split: workgroup z covers K range [z k_chunk, (z + 1) k_chunk) (k_chunk a
@@ -183,11 +201,14 @@ __device__ __forceinline__ void mfma16(float4_t& acc, half8_t a, half8_t b) {
   asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-template <bool TransposeLeft, bool TransposeRight, bool Gelu, bool KTail, bool Split>
+// out may be the addend itself (in place: every element is read and then
+// written by the same lane), but not an operand.
+template <bool TransposeLeft, bool TransposeRight, int Epi, bool KTail, bool Split>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
-    const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K,
-    uint64_t left_batch_stride, uint64_t right_batch_stride, uint32_t k_chunk) {
+    uint16_t* out, const uint16_t* __restrict__ left, const uint16_t* __restrict__ right,
+    uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride,
+    uint32_t k_chunk, const uint16_t* addend, uint64_t addend_batch_stride,
+    uint32_t addend_row_stride) {
   constexpr int BK = 64;
   constexpr int kTileBytes = Tile<BK>::kBytes;
   constexpr int kDma = Tile<BK>::kDmaPerWave;
@@ -388,12 +409,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
     for (int j = 0; j < 8; ++j) {
       half4_t h;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = epilogue<Gelu>(acc[i][j][e]);
+      for (int e = 0; e < 4; ++e) h[e] = epilogue<Epi>(acc[i][j][e]);
       const uint32_t c = 2 * j + g4 / 2;
       *reinterpret_cast<half4_t*>(cst + r * 256 + ((c ^ (r & 15)) << 4) + (g4 % 2) * 8) = h;
     }
   }
   uint16_t* cw = C + (uint64_t)(m0 + wm) * N + n0 + wn;
+  if constexpr (Epi == kEpiAdd) {
+    // The addend's chunks are loaded 8 at a time ahead of their stores
+    // (out may be the addend, so a load cannot move past an earlier store).
+    const uint16_t* aw = addend + batch * addend_batch_stride +
+                         (uint64_t)(m0 + wm) * addend_row_stride + n0 + wn;
+#pragma unroll
+    for (int k0 = 0; k0 < 32; k0 += 8) {
+      u32x4 d[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t v = (k0 + k) * kWave + lane, r = v / 16, c = v % 16;
+        d[k] = m0 + wm + r < M && n0 + wn + c * 8 < N
+                   ? *reinterpret_cast<const u32x4*>(aw + (uint64_t)r * addend_row_stride + c * 8)
+                   : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t v = (k0 + k) * kWave + lane, r = v / 16, c = v % 16;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(cst + r * 256 + ((c ^ (r & 15)) << 4));
+        if (m0 + wm + r < M && n0 + wn + c * 8 < N)
+          __builtin_nontemporal_store(add_f16x8(x, d[k]),
+                                      reinterpret_cast<u32x4*>(cw + (uint64_t)r * N + c * 8));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 32; ++k) {
     const uint32_t v = k * kWave + lane, r = v / 16, c = v % 16;
@@ -407,9 +454,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
 // General fp16 GEMM: 64 x 64 tile, 4 waves of one 32 x 32 MFMA tile each,
 // K step 16, bounds-checked scalar loads.  Any shape, transposes, batches.
 __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ left,
-    const uint16_t* __restrict__ right, uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr,
-    uint64_t left_batch_stride, uint64_t right_batch_stride, uint32_t tiles_n, bool gelu) {
+    uint16_t* out, const uint16_t* __restrict__ left, const uint16_t* __restrict__ right,
+    uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr, uint64_t left_batch_stride,
+    uint64_t right_batch_stride, uint32_t tiles_n, int epi, const uint16_t* addend,
+    uint64_t addend_batch_stride, uint32_t addend_row_stride) {
   __shared__ __attribute__((aligned(16))) half_t As[64][24];
   __shared__ __attribute__((aligned(16))) half_t Bs[64][24];
   const uint64_t batch = blockIdx.y;
@@ -441,41 +489,49 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
   }
   const uint32_t m = m0 + wm + lane % 32;
   if (m >= M) return;
+  const uint16_t* D = addend + batch * addend_batch_stride + (uint64_t)m * addend_row_stride;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const uint32_t n = n0 + wn + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-    if (n < N)
-      C[(uint64_t)m * N + n] =
-          __builtin_bit_cast(uint16_t, gelu ? epilogue<true>(acc[r]) : epilogue<false>(acc[r]));
+    if (n >= N) continue;
+    half_t h = epi == kEpiGelu ? epilogue<kEpiGelu>(acc[r]) : epilogue<kEpiPlain>(acc[r]);
+    if (epi == kEpiAdd) h = add_f16(h, __builtin_bit_cast(half_t, D[n]));
+    C[(uint64_t)m * N + n] = __builtin_bit_cast(uint16_t, h);
   }
 }
 
-template <bool TL, bool TR, bool G, bool Split>
+template <bool TL, bool TR, int Epi, bool Split>
 int launch_fast(hipStream_t stream, const GemmArgs& a, uint32_t splits, uint32_t k_chunk) {
   const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
   const dim3 grid(tiles, a.batches, splits);
   if (a.inner % 64 == 0)
-    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, false, Split>), grid, dim3(kThreads), 0,
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, Epi, false, Split>), grid, dim3(kThreads), 0,
                        stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
                        a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride,
-                       k_chunk);
+                       k_chunk, (const uint16_t*)a.addend, a.addend_batch_stride,
+                       a.addend_row_stride);
   else
-    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, G, true, Split>), grid, dim3(kThreads), 0,
+    hipLaunchKernelGGL((gemm_f16_256_kernel<TL, TR, Epi, true, Split>), grid, dim3(kThreads), 0,
                        stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
                        a.rows, a.columns, a.inner, a.left_batch_stride, a.right_batch_stride,
-                       k_chunk);
+                       k_chunk, (const uint16_t*)a.addend, a.addend_batch_stride,
+                       a.addend_row_stride);
   return hip_status(hipGetLastError());
 }
 
-template <bool G, bool Split>
+template <int Epi, bool Split>
 int dispatch_fast(hipStream_t stream, const GemmArgs& a, uint32_t splits, uint32_t k_chunk) {
   if (!a.transpose_left && !a.transpose_right)
-    return launch_fast<false, false, G, Split>(stream, a, splits, k_chunk);
+    return launch_fast<false, false, Epi, Split>(stream, a, splits, k_chunk);
   if (!a.transpose_left && a.transpose_right)
-    return launch_fast<false, true, G, Split>(stream, a, splits, k_chunk);
+    return launch_fast<false, true, Epi, Split>(stream, a, splits, k_chunk);
   if (a.transpose_left && !a.transpose_right)
-    return launch_fast<true, false, G, Split>(stream, a, splits, k_chunk);
-  return launch_fast<true, true, G, Split>(stream, a, splits, k_chunk);
+    return launch_fast<true, false, Epi, Split>(stream, a, splits, k_chunk);
+  return launch_fast<true, true, Epi, Split>(stream, a, splits, k_chunk);
+}
+
+int epilogue_of(const GemmArgs& a) {
+  return a.addend ? kEpiAdd : a.gelu ? kEpiGelu : kEpiPlain;
 }
 
 // Conditions of the 256 x 256 kernel: 16-byte aligned operands, 32-bit
@@ -489,15 +545,20 @@ bool fast_ok(const GemmArgs& a) {
   const uint64_t b_span = a.transpose_right ? 256ull * a.inner * 2 : (uint64_t)a.inner * a.columns * 2;
   const bool fits = a_span < (1ull << 31) && b_span < (1ull << 31);
   const bool chunked = a.inner % 8 == 0 && a.columns % 8 == 0 && (!a.transpose_left || a.rows % 8 == 0);
-  return aligned && fits && chunked && a.inner > 0;
+  // The add epilogue loads the addend as 16-byte chunks of 8 columns.
+  const bool addend_ok = !a.addend || ((uintptr_t)a.addend % 16 == 0 &&
+                                       a.addend_batch_stride % 8 == 0 && a.addend_row_stride % 8 == 0);
+  return aligned && fits && chunked && addend_ok && a.inner > 0;
 }
 
 // fp32 partials [splits][count] -> fp16 (optionally GELU of the fp16 value):
 // 8 elements per thread, splits summed in order.
-__global__ __launch_bounds__(256) void reduce_splits_f16_kernel(uint16_t* __restrict__ out,
-                                                                const float* __restrict__ parts,
-                                                                uint32_t splits, uint64_t count,
-                                                                bool gelu) {
+// With an addend (out may be the addend): out = add_f16(sum, addend) for the
+// addend element of (batch, row, column), count = batches * rows * columns.
+__global__ __launch_bounds__(256) void reduce_splits_f16_kernel(
+    uint16_t* out, const float* __restrict__ parts, uint32_t splits, uint64_t count, bool gelu,
+    const uint16_t* addend, uint32_t rows, uint32_t columns, uint64_t addend_batch_stride,
+    uint32_t addend_row_stride) {
   const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (i >= count) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -513,7 +574,16 @@ __global__ __launch_bounds__(256) void reduce_splits_f16_kernel(uint16_t* __rest
   }
   half8_t h;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = gelu ? epilogue<true>(acc[e]) : epilogue<false>(acc[e]);
+  for (int e = 0; e < 8; ++e) h[e] = gelu ? epilogue<kEpiGelu>(acc[e]) : epilogue<kEpiPlain>(acc[e]);
+  if (addend) {
+    // columns % 8 == 0, so the 8 elements share one row.
+    const uint64_t row = i / columns, col = i % columns;
+    const uint64_t b = row / rows, m = row % rows;
+    const half8_t d = *reinterpret_cast<const half8_t*>(addend + b * addend_batch_stride +
+                                                        m * addend_row_stride + col);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = add_f16(h[e], d[e]);
+  }
   *reinterpret_cast<half8_t*>(out + i) = h;
 }
 
@@ -527,40 +597,54 @@ int gemm_f16_split_chunk(uint32_t inner, uint32_t splits) {
 
 int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits) {
   if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
-  if (a.batches > 65535 || splits == 0 || splits > 64 || a.gelu) return IPUS_ERROR_INVALID_ARGUMENT;
+  if (a.batches > 65535 || splits == 0 || splits > 64 || a.gelu || a.addend)
+    return IPUS_ERROR_INVALID_ARGUMENT;
   if (!fast_ok(a)) return IPUS_ERROR_UNAVAILABLE;
   const uint32_t k_chunk = (uint32_t)gemm_f16_split_chunk(a.inner, splits);
   // Every split must own at least one k: the plan picks splits so that
   // ceil(K / k_chunk) == splits.
   if ((a.inner + k_chunk - 1) / k_chunk != splits) return IPUS_ERROR_INVALID_ARGUMENT;
-  return dispatch_fast<false, true>(stream, a, splits, k_chunk);
+  return dispatch_fast<kEpiPlain, true>(stream, a, splits, k_chunk);
 }
 
 int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
-                             uint64_t count, bool gelu) {
+                             uint64_t count, bool gelu, const SplitAddend* add) {
   if (count == 0) return 0;
   if (splits == 0 || count % 8 != 0 || (uintptr_t)dst % 16 != 0 || (uintptr_t)parts % 16 != 0)
+    return IPUS_ERROR_INVALID_ARGUMENT;
+  if (add && (gelu || !add->addend || add->rows == 0 || add->columns == 0 ||
+              add->columns % 8 != 0 || count % ((uint64_t)add->rows * add->columns) != 0 ||
+              (uintptr_t)add->addend % 16 != 0 || add->batch_stride % 8 != 0 ||
+              add->row_stride % 8 != 0))
     return IPUS_ERROR_INVALID_ARGUMENT;
   const uint64_t blocks = (count / 8 + 255) / 256;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
   hipLaunchKernelGGL(reduce_splits_f16_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
-                     (uint16_t*)dst, (const float*)parts, splits, count, gelu);
+                     (uint16_t*)dst, (const float*)parts, splits, count, gelu,
+                     add ? (const uint16_t*)add->addend : nullptr, add ? add->rows : 1u,
+                     add ? add->columns : 8u, add ? add->batch_stride : 0ull,
+                     add ? add->row_stride : 0u);
   return hip_status(hipGetLastError());
 }
 
 int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   if (a.batches == 0 || a.rows == 0 || a.columns == 0) return 0;
-  if (a.batches > 65535) return IPUS_ERROR_INVALID_ARGUMENT;
+  if (a.batches > 65535 || (a.gelu && a.addend)) return IPUS_ERROR_INVALID_ARGUMENT;
   // Any M and N on the fast kernel: rows past the edge read as 0 and are not
   // stored.
-  if (fast_ok(a))
-    return a.gelu ? dispatch_fast<true, false>(stream, a, 1, a.inner)
-                  : dispatch_fast<false, false>(stream, a, 1, a.inner);
+  if (fast_ok(a)) {
+    switch (epilogue_of(a)) {
+      case kEpiGelu: return dispatch_fast<kEpiGelu, false>(stream, a, 1, a.inner);
+      case kEpiAdd: return dispatch_fast<kEpiAdd, false>(stream, a, 1, a.inner);
+      default: return dispatch_fast<kEpiPlain, false>(stream, a, 1, a.inner);
+    }
+  }
   const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
   hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
                      stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
                      a.rows, a.columns, a.inner, a.transpose_left, a.transpose_right,
-                     a.left_batch_stride, a.right_batch_stride, tiles_n, a.gelu);
+                     a.left_batch_stride, a.right_batch_stride, tiles_n, epilogue_of(a),
+                     (const uint16_t*)a.addend, a.addend_batch_stride, a.addend_row_stride);
   return hip_status(hipGetLastError());
 }
 
@@ -611,7 +695,7 @@ int launch_gemm_f16_split_noalloc(hipStream_t stream, int device, const GemmArgs
   s.out = parts;
   s.gelu = false;
   if (int e = launch_gemm_f16_split(stream, s, splits)) return e;
-  return launch_reduce_splits_f16(stream, a.out, parts, splits, count, a.gelu);
+  return launch_reduce_splits_f16(stream, a.out, parts, splits, count, a.gelu, nullptr);
 }
 
 }  // namespace ipus

@@ -19,6 +19,21 @@ struct GemmArgs {
   uint32_t rows, columns, inner;
   bool transpose_left, transpose_right;
   bool gelu = false;  // fp16 GEMM only: GELU of the fp16 result in the epilogue
+  // fp16 GEMM only, exclusive with gelu: out = add_f16(addend, fp16 product)
+  // with the addend element at batch * addend_batch_stride + row *
+  // addend_row_stride + column (0 strides broadcast); out may be the addend.
+  const void* addend = nullptr;
+  uint64_t addend_batch_stride = 0;
+  uint32_t addend_row_stride = 0;
+};
+
+// The addend of a split-K reduction (launch_reduce_splits_f16): the partials
+// are [splits][batches][rows][columns].
+struct SplitAddend {
+  const void* addend;
+  uint32_t rows, columns;
+  uint64_t batch_stride;
+  uint32_t row_stride;
 };
 
 struct AttentionArgs {
@@ -44,7 +59,7 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a);
 int gemm_f16_split_chunk(uint32_t inner, uint32_t splits);
 int launch_gemm_f16_split(hipStream_t stream, const GemmArgs& a, uint32_t splits);
 int launch_reduce_splits_f16(hipStream_t stream, void* dst, const void* parts, uint32_t splits,
-                             uint64_t count, bool gelu);
+                             uint64_t count, bool gelu, const SplitAddend* add = nullptr);
 // Declared input format -> row-major (k_memory.hip): `table` is the shard
 // table of tiling.h in device memory; one workgroup row per table shard,
 // `max_shard_elements` sizes the grid.

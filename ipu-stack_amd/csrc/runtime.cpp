@@ -5,11 +5,13 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cctype>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <set>
 #include <string>
 #include <thread>
 #include <vector>
@@ -134,6 +136,40 @@ extern "C" int ipus_context_destroy(ipus_context* ctx) {
   return status;
 }
 
+namespace {
+// Reads the first line of a text file into `out`; false if it is absent or
+// empty.
+bool read_line(const char* path, char* out, size_t size) {
+  FILE* f = fopen(path, "r");
+  if (!f) return false;
+  const bool ok = fgets(out, (int)size, f) != nullptr;
+  fclose(f);
+  if (!ok) return false;
+  out[strcspn(out, "\r\n")] = '\0';
+  return out[0] != '\0';
+}
+
+// Where the runtime reports an empty device name: the product name the
+// amdgpu driver exposes for the device's PCI function, else for the first
+// card that has one, else the architecture and CU count.
+void device_product_name(int device, const hipDeviceProp_t& p, char* out, size_t size) {
+  char bus[64] = {0}, path[160];
+  if (hipDeviceGetPCIBusId(bus, (int)sizeof(bus), device) == hipSuccess && bus[0]) {
+    for (char* c = bus; *c; ++c) *c = (char)tolower((unsigned char)*c);
+    snprintf(path, sizeof(path), "/sys/bus/pci/devices/%s/product_name", bus);
+    if (read_line(path, out, size)) return;
+  }
+  for (int card = 0; card < 64; ++card) {
+    snprintf(path, sizeof(path), "/sys/class/drm/card%d/device/product_name", card);
+    if (read_line(path, out, size)) return;
+  }
+  char arch[32];
+  snprintf(arch, sizeof(arch), "%s", p.gcnArchName);
+  arch[strcspn(arch, ":")] = '\0';
+  snprintf(out, size, "AMD GPU %s (%d CUs)", arch, p.multiProcessorCount);
+}
+}  // namespace
+
 extern "C" int ipus_context_device_info(ipus_context* ctx, ipus_device_info* info) {
   if (!ctx || !info) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   hipDeviceProp_t p;
@@ -141,6 +177,7 @@ extern "C" int ipus_context_device_info(ipus_context* ctx, ipus_device_info* inf
   if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
   memset(info, 0, sizeof(*info));
   snprintf(info->name, sizeof(info->name), "%s", p.name);
+  if (!info->name[0]) device_product_name(ctx->device, p, info->name, sizeof(info->name));
   snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
   info->compute_units = p.multiProcessorCount;
   info->clock_khz = p.clockRate;
@@ -307,12 +344,16 @@ extern "C" int ipus_event_elapsed_ms(ipus_event* start, ipus_event* end, float* 
 namespace {
 
 using Launcher = int (*)(ipus_context*, void*, const void* const*, const uint32_t*);
+// Scalar constraints that validate_kernel_run enforces before any launch
+// (kernel.rs:1384-1435): 0, or the status the run is rejected with.
+using Checker = int (*)(const uint32_t*);
 
 struct KernelEntry {
   const char* symbol;
   int inputs;
   std::vector<const char*> scalars;
   Launcher launch;
+  Checker check = nullptr;
 };
 
 inline float bits_to_float(uint32_t bits) {
@@ -321,22 +362,34 @@ inline float bits_to_float(uint32_t bits) {
   return f;
 }
 
+// GemmArgs from the GEMM symbols' first eight scalars (batches, rows,
+// columns, inner, transpose_left, transpose_right, left and right batch
+// strides).
+int gemm_args(void* out, const void* const* in, const uint32_t* s, GemmArgs* a) {
+  if (s[4] > 1 || s[5] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+  a->out = out;
+  a->left = in[0];
+  a->right = in[1];
+  a->batches = s[0];
+  a->rows = s[1];
+  a->columns = s[2];
+  a->inner = s[3];
+  a->transpose_left = s[4] != 0;
+  a->transpose_right = s[5] != 0;
+  a->left_batch_stride = s[6];
+  a->right_batch_stride = s[7];
+  return 0;
+}
+
+int check_gemm_flags(const uint32_t* s) {
+  return s[4] > 1 || s[5] > 1 ? IPUS_ERROR_INVALID_ARGUMENT : 0;
+}
+
 int run_gemm(ipus_context* ctx, void* out, const void* const* in, const uint32_t* s, bool f16,
              bool gelu = false) {
   GemmArgs a;
+  if (int e = gemm_args(out, in, s, &a)) return e;
   a.gelu = gelu;
-  a.out = out;
-  a.left = in[0];
-  a.right = in[1];
-  a.batches = s[0];
-  a.rows = s[1];
-  a.columns = s[2];
-  a.inner = s[3];
-  a.transpose_left = s[4] != 0;
-  a.transpose_right = s[5] != 0;
-  a.left_batch_stride = s[6];
-  a.right_batch_stride = s[7];
-  if (s[4] > 1 || s[5] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
   return f16 ? launch_gemm_f16(ctx->stream, a) : launch_gemm_f32(ctx->stream, a);
 }
 
@@ -380,6 +433,22 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return run_gemm(c, o, i, s, true, true);
        }},
+      // C = addend + A . B (the reference's accumulate mode, gemm_f16_amp.S:
+      // 43-52, 290-363, as one operator-level launch; also the residual
+      // x + x . W that build_package fuses): the product rounded to fp16,
+      // then added like ipu_stack_add_f16.  The addend may be the output.
+      {"ipu_stack_gemm_f16_accumulate", 3,
+       {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
+        "left_batch_stride", "right_batch_stride", "addend_batch_stride", "addend_row_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         GemmArgs a;
+         if (int e = gemm_args(o, i, s, &a)) return e;
+         a.addend = i[2];
+         a.addend_batch_stride = s[8];
+         a.addend_row_stride = s[9];
+         return launch_gemm_f16(c->stream, a);
+       },
+       check_gemm_flags},
       // Split-K GEMM (no reference counterpart; planned by build_package for
       // few-tile, long-K shapes): fp32 partials float[splits][batches][M][N].
       {"ipu_stack_gemm_f16_split", 2,
@@ -404,8 +473,17 @@ const std::vector<KernelEntry>& registry() {
       // Sum of the split partials rounded to fp16 (GELU of it when gelu = 1).
       {"ipu_stack_reduce_splits_f16", 1, {"splits", "element_count", "gelu"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         if (s[2] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
          return launch_reduce_splits_f16(c->stream, o, i[0], s[0], s[1], s[2] != 0);
+       },
+       [](const uint32_t* s) { return s[2] > 1 ? IPUS_ERROR_INVALID_ARGUMENT : 0; }},
+      // The same sum plus an addend (the split form of
+      // ipu_stack_gemm_f16_accumulate); partials [splits][batches][rows][columns].
+      {"ipu_stack_reduce_splits_accumulate_f16", 2,
+       {"splits", "batches", "rows", "columns", "addend_batch_stride", "addend_row_stride"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         const SplitAddend add{i[1], s[2], s[3], s[4], s[5]};
+         return launch_reduce_splits_f16(c->stream, o, i[0], s[0], (uint64_t)s[1] * s[2] * s[3],
+                                         false, &add);
        }},
       {"ipu_stack_gemm_f32", 2,
        {"batches", "rows", "columns", "inner", "transpose_left", "transpose_right",
@@ -427,16 +505,18 @@ const std::vector<KernelEntry>& registry() {
        }},
       {"ipu_stack_gelu_tanh_approx_f16", 1, {"element_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         // validate_kernel_run: the element count must be even (kernel.rs:1400-1413).
-         if (s[0] % 2 != 0) return IPUS_ERROR_UNSUPPORTED_COUNT;
          return launch_gelu_f16(c->stream, o, i[0], s[0]);
-       }},
+       },
+       // validate_kernel_run: the element count must be even (kernel.rs:1400-1413).
+       [](const uint32_t* s) { return s[0] % 2 != 0 ? IPUS_ERROR_UNSUPPORTED_COUNT : 0; }},
       {"ipu_stack_reduce_sum_f16", 2, {"num_partials", "element_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
-         // partials >= 2 (one initial + >= 1 remote) and count % 8 == 0
-         // (kernel.rs:1414-1423).
-         if (s[0] < 1 || s[1] % 8 != 0) return IPUS_ERROR_UNSUPPORTED_COUNT;
          return launch_reduce_sum_f16(c->stream, o, i[0], i[1], s[0], s[1]);
+       },
+       // partials >= 2 (one initial + >= 1 remote) and count % 8 == 0
+       // (kernel.rs:1414-1423).
+       [](const uint32_t* s) {
+         return s[0] < 1 || s[1] % 8 != 0 ? IPUS_ERROR_UNSUPPORTED_COUNT : 0;
        }},
       {"ipu_stack_rearrange_row_major_f16", 1,
        {"logical_rows", "physical_rows", "target_order", "logical_columns", "physical_columns",
@@ -464,6 +544,15 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const*, const uint32_t* s) {
          return launch_fill_zero(c->stream, o, s[0]);
        }},
+      // The reference's own FillZero step (emit.rs:38, kernel.rs:1223-1229):
+      // bytes / 8 words dealt to six IPU workers, words_per_worker =
+      // bytes / 8 / 6 and remainder_workers = bytes / 8 % 6 (kernel.rs:
+      // 1174-1175), so the zeroed bytes are 8 (6 w + r).
+      {"ipu_stack_fill_zero_u64", 0, {"words_per_worker", "remainder_workers"},
+       [](ipus_context* c, void* o, const void* const*, const uint32_t* s) {
+         return launch_fill_zero(c->stream, o, 8ull * (6ull * s[0] + s[1]));
+       },
+       [](const uint32_t* s) { return s[1] >= 6 ? IPUS_ERROR_INVALID_ARGUMENT : 0; }},
       {"ipu_stack_cast_f32_f16", 1, {"element_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_cast_f32_to_f16(c->stream, o, i[0], s[0]);
@@ -539,21 +628,235 @@ const std::vector<KernelEntry>& registry() {
   return entries;
 }
 
-const KernelEntry* find_kernel(const char* symbol) {
-  if (!symbol) return nullptr;
-  for (const auto& e : registry())
-    if (strcmp(e.symbol, symbol) == 0) return &e;
-  return nullptr;
+// ---- reference per-shape symbols ----
+// The reference links one specialization per operand shape and names it by
+// that shape (KernelBuildPlan::from_program: unpack kernel.rs:321-328,
+// rearrange 374-379 with rearrangement_specialization 1122-1146, flash
+// attention 506-515).  Here one generic kernel serves every shape, so such a
+// symbol resolves to a launch of it whose shape comes from the suffix.
+struct ShapeFamily {
+  const char* prefix;
+  // Suffix fields after the prefix: '#' a decimal u32, 'H' exactly eight
+  // lowercase hex digits ({:08x}); any other character must match itself.
+  const char* pattern;
+  int inputs;
+  std::vector<const char*> scalars;
+  int (*check)(const uint32_t* shape, const uint32_t* scalars);
+  int (*launch)(ipus_context*, void*, const void* const*, const uint32_t* scalars,
+                const uint32_t* shape);
+};
+
+bool parse_suffix(const char* text, const char* pattern, uint32_t* fields) {
+  int n = 0;
+  for (; *pattern; ++pattern) {
+    if (*pattern == '#') {
+      if (*text < '0' || *text > '9') return false;
+      uint64_t v = 0;
+      int digits = 0;
+      while (*text >= '0' && *text <= '9') {
+        v = v * 10 + (uint64_t)(*text++ - '0');
+        if (++digits > 10 || v > 0xffffffffull) return false;
+      }
+      fields[n++] = (uint32_t)v;
+    } else if (*pattern == 'H') {
+      uint32_t v = 0;
+      for (int d = 0; d < 8; ++d, ++text) {
+        const char ch = *text;
+        if (ch >= '0' && ch <= '9') v = v * 16 + (uint32_t)(ch - '0');
+        else if (ch >= 'a' && ch <= 'f') v = v * 16 + (uint32_t)(ch - 'a' + 10);
+        else return false;
+      }
+      fields[n++] = v;
+    } else if (*text++ != *pattern) {
+      return false;
+    }
+  }
+  return *text == '\0';
 }
 
-void fill_info(const KernelEntry& e, ipus_kernel_abi_info* info) {
+const std::vector<ShapeFamily>& shape_families() {
+  static const std::vector<ShapeFamily> families = {
+      // Row-major -> AMP-Left / AMP-TransposedRight / block-major, suffix
+      // o{target}_r{logical rows}_p{physical rows}_c{logical columns}_p{physical
+      // columns}; scalars as the reference passes them (kernel.rs:1351-1361).
+      // A zero logical extent in the suffix is rearrangement_specialization's
+      // runtime form (physical rows 64, fewer logical rows, kernel.rs:
+      // 1129-1139; rearrange_f16.cpp reads the scalar when the define is 0).
+      // The suffix does not name a block shape: target 2 is block-major
+      // {row_block 64, column_block 16}, the only one the reference plans for
+      // this conversion (layout.rs:356-361, 515-527).
+      {"ipu_stack_rearrange_row_major_to_amp_f16_", "o#_r#_p#_c#_p#", 1,
+       {"logical_rows", "physical_rows", "target_order", "logical_columns", "physical_columns"},
+       [](const uint32_t* f, const uint32_t* s) {
+         if (f[0] > 2 || s[2] != f[0]) return IPUS_ERROR_INVALID_ARGUMENT;
+         if (s[1] != f[2] || s[4] != f[4]) return IPUS_ERROR_INVALID_ARGUMENT;
+         if ((f[1] != 0 && s[0] != f[1]) || (f[3] != 0 && s[3] != f[3]))
+           return IPUS_ERROR_INVALID_ARGUMENT;
+         return 0;
+       },
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s, const uint32_t* f) {
+         return launch_rearrange_f16(c->stream, o, i[0], f[0], 64, 16, 1, s[0], s[1], s[3], s[4]);
+       }},
+      // AMP-Output / AMP-TransposedLeft -> row-major, suffix as above with the
+      // source order (kernel.rs:321-328); the codelet compiles every extent in
+      // and takes only `matrices` at run time (unpack_amp_f16.cpp:6-40), so
+      // the scalar extents must equal the suffix.
+      {"ipu_stack_unpack_amp_to_row_major_f16_", "o#_r#_p#_c#_p#", 1,
+       {"matrices", "logical_rows", "physical_rows", "logical_columns", "physical_columns"},
+       [](const uint32_t* f, const uint32_t* s) {
+         if (f[0] > 1) return IPUS_ERROR_INVALID_ARGUMENT;
+         for (int k = 1; k < 5; ++k)
+           if (s[k] != f[k]) return IPUS_ERROR_INVALID_ARGUMENT;
+         return 0;
+       },
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s, const uint32_t* f) {
+         return launch_unpack_f16(c->stream, o, i[0], f[0], s[0], s[1], s[2], s[3], s[4]);
+       }},
+      // Fused non-causal attention with fp32 output, suffix
+      // m{matrices}_q{query rows}_k{key rows}_d{query width}_v{value width}_
+      // {scale bits, {:08x}} (AttentionKernelShape, kernel.rs:121-129,
+      // 986-1040); no scalars.
+      {"ipu_stack_flash_attention_online_f16_", "m#_q#_k#_d#_v#_H", 3, {},
+       [](const uint32_t*, const uint32_t*) { return 0; },
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t*, const uint32_t* f) {
+         AttentionArgs a;
+         a.out = o;
+         a.query = i[0];
+         a.key = i[1];
+         a.value = i[2];
+         a.streams = f[0];
+         a.query_rows = f[1];
+         a.key_rows = f[2];
+         a.width = f[3];
+         a.value_width = f[4];
+         a.scale = bits_to_float(f[5]);
+         a.causal = false;
+         a.output_f16 = false;
+         return launch_attention_f16(c->stream, a);
+       }},
+  };
+  return families;
+}
+
+// Reference symbols this library does not forward, with the reason.
+struct NotForwarded {
+  const char* prefix;
+  bool exact;  // the whole symbol, not a prefix
+  int status;
+  const char* reason;
+};
+
+const NotForwarded kNotForwarded[] = {
+    {"ipu_stack_gemm_f16_init_", false, IPUS_ERROR_TRANSLATED,
+     "a reference tile GEMM codelet (one AMP-Left x block-major shard, shape compiled in, "
+     "kernel.rs:185-193) is translated per operator: one ipu_stack_gemm_f16 over the whole "
+     "M, N, K"},
+    {"ipu_stack_gemm_f16_accumulate_", false, IPUS_ERROR_TRANSLATED,
+     "a reference tile GEMM codelet (accumulate mode) is translated per operator: one "
+     "ipu_stack_gemm_f16_accumulate over the whole M, N, K"},
+    {"ipu_stack_gemm_f32_init_", false, IPUS_ERROR_TRANSLATED,
+     "a reference tile GEMM codelet is translated per operator: one ipu_stack_gemm_f32 over "
+     "the whole M, N, K"},
+    {"ipu_stack_gemm_f32_accumulate_", false, IPUS_ERROR_TRANSLATED,
+     "a reference tile GEMM codelet (accumulate mode) is translated per operator: one "
+     "ipu_stack_gemm_f32 plus ipu_stack_add_f32"},
+    {"ipu_stack_attention_softmax_", false, IPUS_ERROR_TRANSLATED,
+     "a staged-attention codelet (low.rs:2250-2463) is translated: the whole attention is one "
+     "ipu_stack_flash_attention_online_f16 launch"},
+    {"ipu_stack_attention_merge_", false, IPUS_ERROR_TRANSLATED,
+     "a staged-attention codelet (low.rs:2250-2463) is translated: the whole attention is one "
+     "ipu_stack_flash_attention_online_f16 launch"},
+    {"ipu_stack_gemm_f8_", false, IPUS_ERROR_UNAVAILABLE,
+     "fp8 GEMM is KernelAvailability::Required in the reference (kernel.rs:1544-1548): no "
+     "device kernel there or here"},
+    {"ipu_stack_cast_f8_", false, IPUS_ERROR_UNAVAILABLE, "fp8 casts have no device kernel"},
+    {"ipu_stack_unsupported_", false, IPUS_ERROR_UNAVAILABLE,
+     "the reference's placeholder for an unsupported kernel (kernel.rs:1252, 1516)"},
+    {"ipu_stack_cast_identity", true, IPUS_ERROR_UNAVAILABLE,
+     "a cast between equal precisions is KernelAvailability::Required in the reference "
+     "(kernel.rs:1519-1529): no device kernel there or here"},
+    {"ipu_stack_rearrange", true, IPUS_ERROR_UNAVAILABLE,
+     "the reference's generic Rearrange is KernelAvailability::Required (kernel.rs:1365-1370): "
+     "no device kernel there; ipu_stack_rearrange_row_major_f16 and "
+     "ipu_stack_rearrange_to_row_major_f16 cover the row-major conversions"},
+};
+
+// One symbol resolved against the registry: a static entry, or a reference
+// per-shape symbol with its shape fields.
+struct Resolved {
+  const KernelEntry* entry = nullptr;
+  const ShapeFamily* family = nullptr;
+  uint32_t shape[8] = {};
+  int inputs() const { return entry ? entry->inputs : family->inputs; }
+  const std::vector<const char*>& scalars() const {
+    return entry ? entry->scalars : family->scalars;
+  }
+};
+
+int resolve(const char* symbol, Resolved* r) {
+  if (!symbol) return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "kernel symbol is null");
+  for (const auto& e : registry())
+    if (strcmp(e.symbol, symbol) == 0) {
+      r->entry = &e;
+      return 0;
+    }
+  for (const auto& f : shape_families()) {
+    const size_t n = strlen(f.prefix);
+    if (strncmp(symbol, f.prefix, n) != 0) continue;
+    if (!parse_suffix(symbol + n, f.pattern, r->shape))
+      return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "kernel symbol %s: suffix does not match %s%s",
+                  symbol, f.prefix, f.pattern);
+    r->family = &f;
+    return 0;
+  }
+  if (strncmp(symbol, "ipu_stack_cast_", 15) == 0 && strstr(symbol, "_f8"))
+    return fail(IPUS_ERROR_UNAVAILABLE, "kernel %s: fp8 casts have no device kernel", symbol);
+  for (const auto& nf : kNotForwarded)
+    if (nf.exact ? strcmp(symbol, nf.prefix) == 0
+                 : strncmp(symbol, nf.prefix, strlen(nf.prefix)) == 0)
+      return fail(nf.status, "kernel %s: %s", symbol, nf.reason);
+  return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "unknown kernel symbol %s", symbol);
+}
+
+// Interned copies of resolved per-shape symbols, so ipus_kernel_abi can hand
+// out a pointer that stays valid until the process ends.
+const char* intern(const char* symbol) {
+  static std::mutex mutex;
+  static std::set<std::string> names;
+  std::lock_guard<std::mutex> lock(mutex);
+  return names.insert(symbol).first->c_str();
+}
+
+void fill_info(const char* symbol, const Resolved& r, ipus_kernel_abi_info* info) {
   memset(info, 0, sizeof(*info));
-  info->symbol = e.symbol;
-  info->input_count = e.inputs;
-  info->scalar_count = (int)e.scalars.size();
-  for (size_t k = 0; k < e.scalars.size() && k < IPUS_MAX_SCALARS; ++k)
-    info->scalar_names[k] = e.scalars[k];
+  info->symbol = r.entry ? r.entry->symbol : intern(symbol);
+  info->input_count = r.inputs();
+  const auto& scalars = r.scalars();
+  info->scalar_count = (int)scalars.size();
+  for (size_t k = 0; k < scalars.size() && k < IPUS_MAX_SCALARS; ++k)
+    info->scalar_names[k] = scalars[k];
   info->implemented = 1;
+}
+
+// validate_kernel_run (kernel.rs:1384-1435): the symbol resolves, pointer
+// arity and scalar count match its ABI, and the scalars meet its constraints.
+int validate_run(const char* symbol, int input_count, const uint32_t* scalars, int scalar_count,
+                 Resolved* r) {
+  if (int status = resolve(symbol, r)) return status;
+  if (input_count != r->inputs())
+    return fail(IPUS_ERROR_POINTER_ARITY, "kernel run has %d pointer operands, ABI requires %d",
+                input_count, r->inputs());
+  if (scalar_count != (int)r->scalars().size())
+    return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s takes %d scalars, got %d", symbol,
+                (int)r->scalars().size(), scalar_count);
+  if (scalar_count && !scalars) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null scalars");
+  int status = 0;
+  if (r->entry && r->entry->check) status = r->entry->check(scalars);
+  if (r->family) status = r->family->check(r->shape, scalars);
+  if (status == IPUS_ERROR_UNSUPPORTED_COUNT)
+    return fail(status, "kernel %s does not support this element count", symbol);
+  if (status) return fail(status, "kernel %s: scalars do not meet its ABI", symbol);
+  return 0;
 }
 
 }  // namespace
@@ -625,35 +928,36 @@ extern "C" int ipus_kernel_count(int* count) {
 extern "C" int ipus_kernel_abi_at(int index, ipus_kernel_abi_info* info) {
   if (!info || index < 0 || index >= (int)registry().size())
     return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel index %d out of range", index);
-  fill_info(registry()[(size_t)index], info);
+  Resolved r;
+  r.entry = &registry()[(size_t)index];
+  fill_info(r.entry->symbol, r, info);
   return 0;
 }
 
 extern "C" int ipus_kernel_abi(const char* symbol, ipus_kernel_abi_info* info) {
   if (!info) return fail(IPUS_ERROR_INVALID_ARGUMENT, "info is null");
-  const KernelEntry* e = find_kernel(symbol);
-  if (!e) return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "unknown kernel symbol %s", symbol ? symbol : "(null)");
-  fill_info(*e, info);
+  Resolved r;
+  if (int status = resolve(symbol, &r)) return status;
+  fill_info(symbol, r, info);
   return 0;
+}
+
+extern "C" int ipus_validate_kernel_run(const char* symbol, int input_count,
+                                        const uint32_t* scalars, int scalar_count) {
+  Resolved r;
+  return validate_run(symbol, input_count, scalars, scalar_count, &r);
 }
 
 extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
                            const void* const* inputs, int input_count, const uint32_t* scalars,
                            int scalar_count) {
   if (!ctx) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null context");
-  const KernelEntry* e = find_kernel(symbol);
-  if (!e) return fail(IPUS_ERROR_UNKNOWN_SYMBOL, "unknown kernel symbol %s", symbol ? symbol : "(null)");
-  if (input_count != e->inputs)
-    return fail(IPUS_ERROR_POINTER_ARITY, "kernel run has %d pointer operands, ABI requires %d",
-                input_count, e->inputs);
-  if (scalar_count != (int)e->scalars.size())
-    return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s takes %d scalars, got %d", symbol,
-                (int)e->scalars.size(), scalar_count);
+  Resolved r;
+  if (int status = validate_run(symbol, input_count, scalars, scalar_count, &r)) return status;
   if (!output) return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null output", symbol);
   for (int k = 0; k < input_count; ++k)
     if (!inputs || !inputs[k])
       return fail(IPUS_ERROR_INVALID_ARGUMENT, "kernel %s: null input %d", symbol, k);
-  if (scalar_count && !scalars) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null scalars");
   if (ctx->inject_status != 0) {
     if (ctx->inject_after == 0) {
       const int status = ctx->inject_status;
@@ -663,7 +967,9 @@ extern "C" int ipus_launch(ipus_context* ctx, const char* symbol, void* output,
     --ctx->inject_after;
   }
   if (int e = use_device(ctx)) return e;
-  return check_launch(e->launch(ctx, output, inputs, scalars), symbol);
+  const int status = r.entry ? r.entry->launch(ctx, output, inputs, scalars)
+                             : r.family->launch(ctx, output, inputs, scalars, r.shape);
+  return check_launch(status, symbol);
 }
 
 extern "C" int ipus_gemm_f16_split_noalloc(ipus_context* ctx, void* output, const void* left,

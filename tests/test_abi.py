@@ -75,8 +75,13 @@ def test_kernel_registry_matches_reference_abi(ipus):
 
 def test_unknown_symbol_abi(ipus):
     with pytest.raises(ipus.KernelAbiError) as e:
-        ipus.kernel_abi("ipu_stack_unsupported_gelu")
+        ipus.kernel_abi("ipu_stack_no_such_kernel")
     assert e.value.status == ipus.ERROR_UNKNOWN_SYMBOL
+    # the reference's own placeholder for a missing kernel is known, and
+    # unavailable (kernel.rs:1252-1259)
+    with pytest.raises(ipus.KernelAbiError) as e:
+        ipus.kernel_abi("ipu_stack_unsupported_gelu")
+    assert e.value.status == ipus.ERROR_UNAVAILABLE
 
 
 def test_launch_without_context_is_rejected(ipus):

@@ -314,7 +314,7 @@ def test_injected_launch_failure_propagates_and_releases_everything(ipus, oracle
     x = g.host_input("x", [m, d])
     w1 = g.parameter("w1", [d, h])
     w2 = g.parameter("w2", [h, d])
-    g.set_outputs([g.add(g.gemm(g.gelu(g.gemm(x, w1)), w2), x)])
+    g.set_outputs([g.gelu(g.add(g.gemm(g.gelu(g.gemm(x, w1)), w2), x))])
     pkg = ipus.build_package(g)
     assert len(pkg.steps) == 3
     feeds = {"x": synth(ipus, m * d, 51, 1).reshape(m, d),
@@ -481,3 +481,29 @@ def test_reference_attention_smoke_from_reference_layout_bytes(ipus, oracle, ctx
                             heads, qr, kr, d, d)
     err = np.abs(y.reshape(-1) - want.reshape(-1))
     assert float(err.max()) <= 0.012 and float(np.sqrt(np.mean(err ** 2))) <= 0.003
+
+
+def test_residual_and_bias_packages_fuse_and_match_two_launches(ipus, oracle, ctx):
+    """x + x . W and x . W + bias plan one accumulate launch each; the fused
+    package equals the GEMM and Add kernels run one after the other."""
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [2, 300, 256])
+    w = g.parameter("w", [256, 256])
+    bias = g.parameter("bias", [256])
+    g.set_outputs([g.add(x, g.gemm(x, w)), g.add(g.gemm(x, w), bias)])
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_accumulate"] * 2
+    xs = synth(ipus, 2 * 300 * 256, 53, 1).reshape(2, 300, 256)
+    ws = synth(ipus, 256 * 256, 53, 2, scale=0.05).reshape(256, 256)
+    bs = synth(ipus, 256, 53, 3)
+    _, (res, biased) = run_package(ipus, ctx, g, {"x": xs, "w": ws, "bias": bs})
+    n = 2 * 300 * 256
+    dx, dw, db = ctx.upload(xs), ctx.upload(ws), ctx.upload(bs)
+    prod, want = ctx.alloc(n * 2), ctx.alloc(n * 2)
+    ctx.launch("ipu_stack_gemm_f16", prod, [dx, dw], [2, 300, 256, 256, 0, 0, 300 * 256, 0])
+    ctx.launch("ipu_stack_add_f16", want, [dx, prod], [n, n, n])
+    assert np.array_equal(res.reshape(-1), want.download(np.uint16))
+    ctx.launch("ipu_stack_add_f16", want, [prod, db], [n, n, 256])
+    assert np.array_equal(biased.reshape(-1), want.download(np.uint16))
+    for b in (dx, dw, db, prod, want):
+        b.free()

@@ -687,3 +687,60 @@ def test_gemm_k_tail_ignores_memory_after_the_operands(ipus, oracle, ctx, M, N, 
     assert fp16_close(got, want, FP16_TOL)
     for x in (da, db, out):
         x.free()
+
+
+# ---------------------------------------------------------------------------
+# GEMM accumulate (C = addend + A . B): bit-identical to GEMM then Add
+# ---------------------------------------------------------------------------
+def _addend_layout(kind, batches, M, N):
+    """(element count, batch stride, row stride) of an addend that is a full
+    [B, M, N] tensor, one [M, N] matrix for every batch, or one [N] row."""
+    return {"full": (batches * M * N, M * N, N), "matrix": (M * N, 0, N),
+            "rows": (N, 0, 0)}[kind]
+
+
+@pytest.mark.parametrize("M,N,K,tl,tr,batches,kind", [
+    (256, 256, 256, 0, 0, 1, "full"), (300, 264, 72, 0, 0, 1, "full"),
+    (264, 520, 200, 1, 0, 2, "full"), (130, 264, 128, 0, 1, 3, "matrix"),
+    (128, 512, 256, 1, 1, 1, "rows"), (100, 60, 40, 0, 0, 2, "full"),
+    (17, 19, 72, 0, 1, 1, "rows"), (1024, 1024, 1024, 0, 0, 1, "full")])
+def test_gemm_f16_accumulate_bit_identical_to_gemm_then_add(ipus, ctx, M, N, K, tl, tr,
+                                                            batches, kind):
+    a = synth(ipus, batches * M * K, 51, 1)
+    b = synth(ipus, batches * K * N, 51, 2, 0, 0.2)
+    count, abs_, ars = _addend_layout(kind, batches, M, N)
+    d = synth(ipus, count, 51, 3, 1)
+    sc = [batches, M, N, K, tl, tr, M * K, K * N]
+    prod = run(ctx, "ipu_stack_gemm_f16", batches * M * N * 2, [a, b], sc)
+    total = batches * M * N
+    want = run(ctx, "ipu_stack_add_f16", total * 2, [prod, d], [total, total, count])
+    got = run(ctx, "ipu_stack_gemm_f16_accumulate", total * 2, [a, b, d], sc + [abs_, ars])
+    assert np.array_equal(got, want)
+    if kind == "full":
+        # in place: the output is the addend (the reference's accumulate mode)
+        da, db = ctx.upload(a), ctx.upload(b)
+        c = ctx.upload(d)
+        ctx.launch("ipu_stack_gemm_f16_accumulate", c, [da, db, c], sc + [abs_, ars])
+        assert np.array_equal(c.download(np.uint16), want)
+        for x in (da, db, c):
+            x.free()
+
+
+@pytest.mark.parametrize("M,N,K,splits,kind", [(729, 1152, 4304, 4, "full"),
+                                               (256, 256, 8192, 8, "rows")])
+def test_split_accumulate_bit_identical_to_reduce_then_add(ipus, ctx, M, N, K, splits, kind):
+    a = synth(ipus, M * K, 52, 1)
+    b = synth(ipus, K * N, 52, 2, 0, 0.1)
+    count, abs_, ars = _addend_layout(kind, 1, M, N)
+    d = synth(ipus, count, 52, 3, 1)
+    da, db, dd = ctx.upload(a), ctx.upload(b), ctx.upload(d)
+    parts = ctx.alloc(splits * M * N * 4)
+    ctx.launch("ipu_stack_gemm_f16_split", parts, [da, db], [1, M, N, K, 0, 0, 0, 0, splits])
+    prod, want, got = ctx.alloc(M * N * 2), ctx.alloc(M * N * 2), ctx.alloc(M * N * 2)
+    ctx.launch("ipu_stack_reduce_splits_f16", prod, [parts], [splits, M * N, 0])
+    ctx.launch("ipu_stack_add_f16", want, [prod, dd], [M * N, M * N, count])
+    ctx.launch("ipu_stack_reduce_splits_accumulate_f16", got, [parts, dd],
+               [splits, 1, M, N, abs_, ars])
+    assert np.array_equal(got.download(np.uint16), want.download(np.uint16))
+    for x in (da, db, dd, parts, prod, want, got):
+        x.free()

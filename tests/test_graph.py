@@ -255,6 +255,72 @@ def test_gemm_gelu_fusion_needs_a_private_result(ipus):
     assert "ipu_stack_gemm_f16_gelu" not in steps
 
 
+def test_gemm_add_fusion_plans(ipus):
+    """A Gemm read only by the Add after it becomes one accumulate launch
+    (C = addend + A . B) when the addend broadcasts as whole rows or
+    matrices; otherwise both launches stay."""
+    def steps(build, config=None):
+        g = ipus.ComputeGraph()
+        g.set_outputs([build(g)])
+        pkg = ipus.build_package(g, config) if config else ipus.build_package(g)
+        return [(s[0], s[2]) for s in pkg.steps]
+
+    # residual x + x . W per Repeat layer: one launch a layer (graph.rs:12-33)
+    g = ipus.ComputeGraph()
+    x = g.host_input("x", [64, 64])
+    seq = g.value_sequence("layers", [g.parameter(f"w{i}", [64, 64]) for i in range(4)])
+    g.set_outputs(g.repeat(4, [x], [], [seq], lambda b, a: [
+        b.add(a.carried[0], b.gemm(a.carried[0], a.iterated[0]))]))
+    pkg = ipus.build_package(g)
+    assert [s[0] for s in pkg.steps] == ["ipu_stack_gemm_f16_accumulate"] * 4
+    assert all(s[1] == 3 and s[2][8:] == (0, 64) for s in pkg.steps)
+    # bias over the rows, either operand order
+    for order in (0, 1):
+        def bias(g, order=order):
+            y = g.gemm(g.host_input("x", [128, 256]), g.parameter("w", [256, 512]))
+            b = g.parameter("b", [512])
+            return g.add(y, b) if order == 0 else g.add(b, y)
+        assert steps(bias) == [("ipu_stack_gemm_f16_accumulate",
+                                (1, 128, 512, 256, 0, 0, 0, 0, 0, 0))]
+    # batched product and a batched residual
+    def batched(g):
+        x = g.host_input("x", [2, 3, 64, 64])
+        return g.add(g.gemm(x, g.parameter("w", [64, 32])), g.host_input("r", [2, 3, 64, 32]))
+    assert steps(batched) == [("ipu_stack_gemm_f16_accumulate",
+                               (6, 64, 32, 64, 0, 0, 4096, 0, 2048, 32))]
+    # the addend broadcast over the batch
+    def shared(g):
+        x = g.host_input("x", [2, 3, 64, 64])
+        return g.add(g.gemm(x, g.parameter("w", [64, 32])), g.host_input("r", [64, 32]))
+    assert steps(shared)[0][1][8:] == (0, 32)
+    # not expressible: a column broadcast, a partial batch broadcast
+    def column(g):
+        y = g.gemm(g.host_input("x", [64, 64]), g.parameter("w", [64, 64]))
+        return g.add(y, g.host_input("c", [64, 1]))
+    assert [s[0] for s in steps(column)] == ["ipu_stack_gemm_f16", "ipu_stack_add_broadcast_f16"]
+    def partial(g):
+        y = g.gemm(g.host_input("x", [2, 3, 64, 64]), g.parameter("w", [64, 64]))
+        return g.add(y, g.host_input("r", [2, 1, 64, 64]))
+    assert [s[0] for s in steps(partial)] == ["ipu_stack_gemm_f16", "ipu_stack_add_broadcast_f16"]
+    # the product also read elsewhere, and fp32 compute: no fusion
+    def shared_product(g):
+        y = g.gemm(g.host_input("x", [64, 64]), g.parameter("w", [64, 64]))
+        return g.add(g.add(y, g.host_input("r", [64, 64])), y)
+    assert steps(shared_product)[0][0] == "ipu_stack_gemm_f16"
+    def plain(g):
+        y = g.gemm(g.host_input("x", [64, 64]), g.parameter("w", [64, 64]))
+        return g.add(y, g.host_input("r", [64, 64]))
+    assert "ipu_stack_gemm_f16_accumulate" not in [
+        s[0] for s in steps(plain, ipus.PackageConfig(compute_precision="f32"))]
+    # a split-K GEMM fuses into its reduction
+    def split(g):
+        y = g.gemm(g.host_input("x", [729, 4304]), g.parameter("w", [4304, 1152]))
+        return g.add(g.host_input("r", [729, 1152]), y)
+    (s0, _), (s1, sc) = steps(split)
+    assert s0 == "ipu_stack_gemm_f16_split" and s1 == "ipu_stack_reduce_splits_accumulate_f16"
+    assert sc[1:] == (1, 729, 1152, 0, 1152)
+
+
 def _projected_attention(ipus, b=2, s=128, d=256, heads=2):
     g = ipus.ComputeGraph()
     x = g.host_input("x", [b, s, d])
