@@ -127,13 +127,16 @@ def gemm_scalars(n, m=None, k=None):
     return [1, m, n, k, 0, 0, 0, 0]
 
 
-def bench_gemm_f16(ipus, ctx, n, steps, warmup, per_launch=False, repeats=5, settle=0):
+def bench_gemm_f16(ipus, ctx, n, steps, warmup, per_launch=False, repeats=5, settle=0,
+                   tl=False, tr=False):
     """`settle` untimed launches and a synchronisation before timed()'s own
-    warmups (the headline's settle phase)."""
+    warmups (the headline's settle phase); tl / tr: A and / or B stored
+    transposed (the same bytes read as the other layout)."""
     a = ctx.upload(ipus.synth_f16(n * n, 2024, 1, ipus.UNIFORM))
     b = ctx.upload(ipus.synth_f16(n * n, 2024, 2, ipus.UNIFORM))
     c = ctx.alloc(n * n * 2)
-    fn = lambda i: ctx.launch("ipu_stack_gemm_f16", c, [a, b], gemm_scalars(n))  # noqa: E731
+    sc = [1, n, n, n, int(tl), int(tr), 0, 0]
+    fn = lambda i: ctx.launch("ipu_stack_gemm_f16", c, [a, b], sc)  # noqa: E731
     ms = timed(ctx, fn, steps, warmup, per_launch=per_launch, repeats=repeats, settle=settle)
     for x in (a, b, c):
         x.free()
@@ -659,7 +662,7 @@ SETTLE_LAUNCHES = 60
 # causal S4096 rate climbs from ~900 to ~1,040 TFLOP/s over ~60 launches).
 ATTENTION_SETTLE_LAUNCHES = 200
 
-LEGS = ("mfma_calibration", "gemm_f32_4096", "attention_causal_s4096",
+LEGS = ("mfma_calibration", "gemm_f16_layouts", "gemm_f32_4096", "attention_causal_s4096",
         "attention_noncausal_s2048", "memory_chain", "amp_layouts", "gelu_4096x16384",
         "mlp_graph", "gemm_f16_256")
 
@@ -679,6 +682,15 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
             cal["headline_frac_of_uniform"] = round(headline_tflops / cal["uniform"]["tflops"], 4)
         results["mfma_calibration"] = cal
         log(f"mfma calibration: {cal}")
+    if want("gemm_f16_layouts"):
+        # The headline GEMM with B, A or both stored transposed (NN is the
+        # headline itself): the same kernel template reads K-contiguous rows
+        # with ds_read_b128 and MN-contiguous ones with ds_read_b64_tr_b16.
+        for name, tl, tr in (("nt", False, True), ("tn", True, False), ("tt", True, True)):
+            t = bench_gemm_f16(ipus, ctx, n, sub_steps, 2, settle=SETTLE_LAUNCHES, tl=tl, tr=tr)
+            results[f"gemm_f16_8192_{name}"] = leg_entry(t, 2.0 * n ** 3, "tflops",
+                                                         PEAK_FP16_TFLOPS)
+            log(f"gemm_f16 8192^3 {name.upper()}: {results[f'gemm_f16_8192_{name}']}")
     if want("gemm_f32_4096"):
         t = bench_gemm_f32(ipus, ctx, 4096, sub_steps, 2, settle=SETTLE_LAUNCHES)
         results["gemm_f32_4096"] = leg_entry(t, 2.0 * 4096 ** 3, "tflops", PEAK_FP32_TFLOPS)
@@ -849,7 +861,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic, "traffic_source": traffic_note,
-                     "kernel": "gemm_f16_256_kernel<false, false, false, false, false>",
+                     "kernel": "gemm_f16_256_kernel<false, false, 0, false, false>",
                      "ms_mean": round(t.mean, 5)},
         "results": results,
         "device": {"name": name, "arch": info["arch"], "cus": info["compute_units"]},

@@ -19,6 +19,20 @@ namespace ipus {
 namespace {
 
 constexpr int kThreads = 256;
+// Rows of the tiles of the AMP-Left / AMP-TransposedRight conversions and
+// the AMP-Output unpack: 256 rows x 64 columns per workgroup, 8 chunks of 16
+// bytes per thread, all loaded before any is stored.
+// Rows of the AMP-Output unpack's tiles (32 rows x 64 columns: one 16-byte
+// chunk per thread; 64-row tiles with two chunks in flight per thread
+// measured 5.35 TB/s against 5.40, 256-row tiles 2.8).
+constexpr uint32_t kAmpTileRows = 32;
+
+// LDS bytes a workgroup requests (on top of its static LDS) so that at most
+// `workgroups` of it share a CU: the launch keeps no more than that many
+// resident, whatever its registers would allow (160 KiB of LDS per CU).
+constexpr uint32_t occupancy_lds(uint32_t workgroups, uint32_t static_bytes) {
+  return 163840u / (workgroups + 1) + 1 - static_bytes;
+}
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
@@ -59,20 +73,26 @@ __device__ __forceinline__ void store16_nt(void* p, u32x4 v) {
 // A wave owns a 64x64 tile; lane (rc = lane % 8, cc = lane / 8) owns the 8x8
 // block at rows 8*rc, columns 8*cc.  For each of the 8 loads the wave reads 8
 // rows x 128 contiguous bytes; for each store it writes 8 rows x 128 bytes.
-// A workgroup stacks its 4 waves' tiles vertically (256 rows x 64 columns),
-// so together they write 512-byte runs of each destination row (128 x 128
-// square blocks: 5.15 TB/s; 64 x 256: 4.90; 256 x 64: 5.25, 5.4 with
-// non-temporal loads).
+// A workgroup of 8 waves stacks their tiles vertically (512 rows x 64
+// columns), so together they write 1 KiB runs of each destination row, and
+// one workgroup runs per CU (the launch requests LDS it does not use, see
+// occupancy_lds): fewer tiles in flight at once keep the reads and writes
+// of the whole chip on fewer DRAM rows.  Measured on 8192^2 fp16, TB/s:
+// 256 x 64 tiles of 4 waves 5.40 with up to 6 workgroups per CU, 5.70 with
+// 3; 512 x 64 with one 5.81-5.83 (with two 5.48; 1024 x 64, 768 x 64 and
+// 512 x 128 with one: 5.36, 5.43, 5.39; 128 x 128 with 3-4: 5.21; a
+// persistent grid loading the next tile before storing the current one:
+// 4.9-5.5).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void transpose_f16_kernel(
+constexpr uint32_t kTransposeWaves = 8;
+__global__ __launch_bounds__(64 * kTransposeWaves) void transpose_f16_kernel(
     uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t columns,
     uint32_t tiles_c) {
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t lane = threadIdx.x % kWave;
-  // Block covers 256 x 64 (4 wave tiles stacked by rows).
   uint32_t tr, tc;
   tile_of_block(tiles_c, 7, &tr, &tc);
-  const uint32_t block_r = tr * 256 + wave * 64;
+  const uint32_t block_r = tr * (64 * kTransposeWaves) + wave * 64;
   const uint32_t block_c = tc * 64;
   const uint64_t matrix = blockIdx.y;
   const uint32_t r0 = block_r + (lane % 8) * 8;
@@ -133,7 +153,8 @@ __global__ __launch_bounds__(kThreads) void block_major_f16_kernel(
 // contiguous run of 32 KiB starting at element tr * columns * 64 + tc * 16384
 // (its 256 / cb column blocks are consecutive): the register-transposed 8x8
 // blocks are placed in LDS at their offsets in that run, and the run is then
-// written with whole-line streaming stores.
+// written with whole-line streaming stores.  At most three workgroups share
+// a CU (occupancy_lds; five by LDS: 5.96-5.99 TB/s, three 6.09, two 6.08-6.11).
 // LDS slot of 16-byte chunk p of the staged run: XOR-swizzled so that the
 // transposed 8x8 blocks a 16-lane group stores (8 column chunks x 2 row
 // halves) hit distinct bank groups for column blocks 16 and 64 (unswizzled:
@@ -142,10 +163,11 @@ __device__ __forceinline__ uint32_t stage_chunk(uint32_t p) {
   return p ^ ((((p >> 4) ^ (p >> 6)) & 7u) << 1);
 }
 
+constexpr uint32_t kBlockMajorStaticLds = 64 * 256 * 2;
 __global__ __launch_bounds__(kThreads) void block_major64_f16_kernel(
     uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t columns,
     uint32_t column_block, uint32_t tiles_c) {
-  __shared__ __attribute__((aligned(16))) uint8_t stage[64 * 256 * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kBlockMajorStaticLds];
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
@@ -235,61 +257,89 @@ __global__ __launch_bounds__(kThreads) void unpack_f16_kernel(
 // elements.  AMP-Left and AMP-TransposedRight keep every run of 8 columns
 // (8-aligned) contiguous (panels of 16 columns, 16 x 16 blocks stored row by
 // row), so a chunk of a row-major row is a chunk of the stored tensor.  A
-// workgroup takes a tile 64 columns wide: each row-major row of the tile is
-// one 128-byte line, and the stored side of the tile is 4 panels of 64 rows
-// x 32 bytes (AMP-Left) or 2 x 4 blocks of 512 bytes (TransposedRight), so
-// both sides are read and written in runs of 256 bytes or more per wave.
+// workgroup takes a tile of kAmpTileRows rows x 64 columns: each row-major
+// row of the tile is one 128-byte line, and the stored side is 4 panels of
+// kAmpTileRows rows x 32 bytes (AMP-Left) or runs of 4 blocks of 512 bytes
+// (TransposedRight), so both sides are read and written in runs of 256
+// bytes or more per wave instruction.  Each thread loads its 8 chunks before
+// it stores any (64 x 64 tiles, 2 chunks per thread: 5.0 / 5.8 TB/s).
 // ToRowMajor runs the same map the other way (stored -> row-major).
 // AMP-Left folds matrices into the rows (storage.rs:250-266), so `rows` is
 // all matrices' rows and blockIdx.y is 0; TransposedRight is per matrix.
 // ---------------------------------------------------------------------------
-template <uint32_t Order, bool ToRowMajor>
+template <uint32_t Order, bool ToRowMajor, uint32_t TileRows, uint32_t TileCols>
 __global__ __launch_bounds__(kThreads) void amp_tile_f16_kernel(uint16_t* __restrict__ dst,
                                                                 const uint16_t* __restrict__ src,
                                                                 uint32_t rows, uint32_t columns,
                                                                 uint32_t tiles_c) {
-  constexpr uint32_t kTileRows = Order == kOrderAmpLeft ? 64 : 32;
-  constexpr uint32_t kPer = kTileRows * 8 / kThreads;  // chunks per thread
-  const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  constexpr uint32_t kRowChunks = TileCols / 8;
+  constexpr uint32_t kPer = TileRows * kRowChunks / kThreads;  // chunks per thread, all in flight
+  static_assert(kPer >= 1 && TileRows * kRowChunks % kThreads == 0, "whole chunks per thread");
+  uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  // AMP-Left: XCD-regrouped diagonal order, as the transpose (its stored
+  // side is a transpose of 32-byte pieces; plain order 5.0 TB/s, 5.35 so).
+  if (Order == kOrderAmpLeft) tile_of_block(tiles_c, 7, &tr, &tc);
   const uint64_t me = (uint64_t)rows * columns;
   src += blockIdx.y * me;
   dst += blockIdx.y * me;
+  u32x4 v[kPer];
+  uint64_t to[kPer];
+  bool ok[kPer];
 #pragma unroll
   for (uint32_t i = 0; i < kPer; ++i) {
     const uint32_t k = threadIdx.x + kThreads * i;
-    const uint32_t r = tr * kTileRows + k / 8, c = tc * 64 + (k % 8) * 8;
-    if (r >= rows || c >= columns) continue;
+    const uint32_t r = tr * TileRows + k / kRowChunks, c = tc * TileCols + (k % kRowChunks) * 8;
+    ok[i] = r < rows && c < columns;
     const uint64_t row_major = (uint64_t)r * columns + c;
     const uint64_t stored = Order == kOrderAmpLeft
                                 ? amp_left_index(rows, r, c)
                                 : amp_transposed_right_index(rows, columns, r, c);
-    if constexpr (ToRowMajor)
-      store16_nt(dst + row_major, load16_nt(src + stored));
-    else
-      store16_nt(dst + stored, load16_nt(src + row_major));
+    to[i] = ToRowMajor ? row_major : stored;
+    if (ok[i]) v[i] = load16_nt(src + (ToRowMajor ? stored : row_major));
   }
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i)
+    if (ok[i]) store16_nt(dst + to[i], v[i]);
 }
 
 // Unpack AMP-Output (pair-permuted 16-column micros, storage.rs:329-340),
-// unpadded and aligned: a thread moves one micro (32 bytes), restoring the
-// pair order in registers: logical pair p sits at physical pair
-// (p % 4) * 2 + p / 4.  A workgroup takes 64 rows x 64 columns: four
-// threads cover a 128-byte row line, and a wave reads 512-byte runs (16
-// rows) of each of the tile's four panels.
+// unpadded and aligned.  Logical pair p of a micro sits at physical pair
+// (p % 4) * 2 + p / 4, so each 16-byte half of the row-major micro takes two
+// words from each stored half.  Two adjacent lanes take one micro, one
+// stored half each, and swap two words (DPP within the lane pair); then
+// eight lanes write one whole 128-byte row line (64 columns), and a wave
+// instruction writes 8 whole lines and reads 4 runs of 256 bytes (8 rows of
+// each of the tile's 4 panels).  A workgroup takes 256 rows x 64 columns,
+// 8 loads in flight per thread.
 __global__ __launch_bounds__(kThreads) void unpack_amp_output_f16_kernel(
     uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows,
     uint32_t columns, uint32_t tiles_c) {
+  constexpr uint32_t kPasses = kAmpTileRows / 32;
   const uint32_t tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
-  const uint32_t r = tr * 64 + threadIdx.x / 4, c = tc * 64 + (threadIdx.x % 4) * kMicro;
-  if (r >= rows || c >= columns) return;
+  const uint32_t half = threadIdx.x % 2, micro = threadIdx.x / 2 % 4;
+  const uint32_t c = tc * 64 + micro * kMicro;
   const uint64_t me = (uint64_t)rows * columns;
-  const uint16_t* s = src + blockIdx.y * me + amp_output_index(rows, r, c);
-  const u32x4 a = load16_nt(s), b = load16_nt(s + 8);
-  // word = one pair; logical pairs 0-3 <- physical 0, 2, 4, 6, pairs 4-7 <- 1, 3, 5, 7
-  const u32x4 lo = {a[0], a[2], b[0], b[2]}, hi = {a[1], a[3], b[1], b[3]};
-  uint16_t* d = dst + blockIdx.y * me + (uint64_t)r * columns + c;
-  store16_nt(d, lo);
-  store16_nt(d + 8, hi);
+  const uint16_t* s = src + blockIdx.y * me;
+  uint16_t* d = dst + blockIdx.y * me;
+  u32x4 v[kPasses];
+#pragma unroll
+  for (uint32_t i = 0; i < kPasses; ++i) {
+    const uint32_t r = tr * kAmpTileRows + 32 * i + threadIdx.x / 8;
+    if (r < rows && c < columns) v[i] = load16_nt(s + amp_output_index(rows, r, c) + half * 8);
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kPasses; ++i) {
+    const uint32_t r = tr * kAmpTileRows + 32 * i + threadIdx.x / 8;
+    // Half 0 holds logical pairs 0, 4, 1, 5 and keeps 0, 1 (words 0, 2);
+    // half 1 holds 2, 6, 3, 7 and keeps 6, 7 (words 1, 3).  Each sends the
+    // other two words to its partner (quad_perm [1, 0, 3, 2]).
+    const uint32_t x0 = half == 0 ? v[i][1] : v[i][0];
+    const uint32_t x1 = half == 0 ? v[i][3] : v[i][2];
+    const uint32_t y0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x0, 0xB1, 0xF, 0xF, true);
+    const uint32_t y1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x1, 0xB1, 0xF, 0xF, true);
+    const u32x4 out = half == 0 ? u32x4{v[i][0], v[i][2], y0, y1} : u32x4{y0, y1, v[i][1], v[i][3]};
+    if (r < rows && c < columns) store16_nt(d + (uint64_t)r * columns + c + half * 8, out);
+  }
 }
 
 // Unpack AMP-TransposedLeft (AMP-Left of the transpose, storage.rs:326-328),
@@ -757,9 +807,10 @@ int launch_transpose_f16(hipStream_t stream, void* dst, const void* src, uint32_
                          uint32_t rows, uint32_t columns) {
   if (matrices == 0 || rows == 0 || columns == 0) return 0;
   if (rows % 8 == 0 && columns % 8 == 0 && aligned16(dst) && aligned16(src) && matrices <= 65535) {
-    const uint32_t tiles_r = ceil_div(rows, 256), tiles_c = ceil_div(columns, 64);
-    hipLaunchKernelGGL(transpose_f16_kernel, dim3(tiles_r * tiles_c, matrices), dim3(kThreads), 0,
-                       stream, (uint16_t*)dst, (const uint16_t*)src, rows, columns, tiles_c);
+    const uint32_t tiles_r = ceil_div(rows, 64 * kTransposeWaves), tiles_c = ceil_div(columns, 64);
+    hipLaunchKernelGGL(transpose_f16_kernel, dim3(tiles_r * tiles_c, matrices),
+                       dim3(64 * kTransposeWaves), occupancy_lds(1, 0), stream, (uint16_t*)dst,
+                       (const uint16_t*)src, rows, columns, tiles_c);
   } else {
     const uint64_t total = (uint64_t)matrices * rows * columns;
     hipLaunchKernelGGL(transpose_f16_scalar_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads),
@@ -774,19 +825,20 @@ int launch_transpose_f16(hipStream_t stream, void* dst, const void* src, uint32_
 template <bool ToRowMajor>
 bool launch_amp_tile(hipStream_t stream, void* dst, const void* src, uint32_t order,
                      uint32_t matrices, uint32_t rows, uint32_t columns) {
-  const uint32_t tiles_c = ceil_div(columns, 64);
   if (order == kOrderAmpLeft) {
+    const uint32_t tiles_c = ceil_div(columns, 64);
     const uint64_t flat = (uint64_t)matrices * rows;
     const uint64_t tiles = ceil_div(flat, 64) * (uint64_t)tiles_c;
     if (flat > 0xffffffffull || tiles > 0x7fffffffull) return false;
-    hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpLeft, ToRowMajor>), dim3((uint32_t)tiles),
-                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
-                       (uint32_t)flat, columns, tiles_c);
+    hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpLeft, ToRowMajor, 64, 64>),
+                       dim3((uint32_t)tiles), dim3(kThreads), 0, stream, (uint16_t*)dst,
+                       (const uint16_t*)src, (uint32_t)flat, columns, tiles_c);
     return true;
   }
+  const uint32_t tiles_c = ceil_div(columns, 64);
   const uint64_t tiles = (uint64_t)ceil_div(rows, 32) * tiles_c;
   if (tiles > 0x7fffffffull || matrices > 65535) return false;
-  hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpTransposedRight, ToRowMajor>),
+  hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpTransposedRight, ToRowMajor, 32, 64>),
                      dim3((uint32_t)tiles, matrices), dim3(kThreads), 0, stream, (uint16_t*)dst,
                      (const uint16_t*)src, rows, columns, tiles_c);
   return true;
@@ -819,7 +871,7 @@ int launch_rearrange_f16(hipStream_t stream, void* dst, const void* src, uint32_
       physical_columns % 256 == 0) {
     const uint32_t tiles_r = physical_rows / 64, tiles_c = physical_columns / 256;
     hipLaunchKernelGGL(block_major64_f16_kernel, dim3(tiles_r * tiles_c, matrices), dim3(kThreads),
-                       0, stream, (uint16_t*)dst, (const uint16_t*)src, physical_columns,
+                       occupancy_lds(3, kBlockMajorStaticLds), stream, (uint16_t*)dst, (const uint16_t*)src, physical_columns,
                        column_block, tiles_c);
   } else if (fast_block_major) {
     const uint32_t tiles_r = ceil_div(physical_rows, 64), tiles_c = ceil_div(physical_columns, 256);
@@ -856,7 +908,8 @@ int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t s
   if (total == 0) return 0;
   const bool unpadded = logical_rows == physical_rows && logical_columns == physical_columns &&
                         aligned16(dst) && aligned16(src);
-  const uint64_t out_tiles = (uint64_t)ceil_div(physical_rows, 64) * ceil_div(physical_columns, 64);
+  const uint64_t out_tiles =
+      (uint64_t)ceil_div(physical_rows, kAmpTileRows) * ceil_div(physical_columns, 64);
   if (unpadded && source_order == kUnpackAmpOutput && out_tiles <= 0x7fffffffull &&
       matrices <= 65535) {
     const uint32_t tiles_c = ceil_div(physical_columns, 64);
