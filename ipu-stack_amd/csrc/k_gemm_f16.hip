@@ -500,6 +500,188 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
   }
 }
 
+// Small fp16 GEMM: 64 x 64 or 32 x 32 output tiles, for shapes with fewer
+// 256 x 256 tiles than kSmallBelowTiles, which would keep few of the 256
+// CUs busy (configs[0]'s 256^3 is a single such tile).  256 threads = 4
+// waves in a 2 x 2 grid, each (Tile / 2)^2 of C as tiles of
+// v_mfma_f32_16x16x32_f16 (C^T as in the 256 x 256 kernel, so a lane holds
+// 4 consecutive columns).  K runs in chunks of 256: a chunk's
+// operand tiles (4 steps of 64) are loaded to registers, 16 loads of 16
+// bytes per thread in flight at once, stored to four LDS stages, and
+// computed while the next chunk's loads are in flight; a K of at most 256
+// takes one memory round trip.  K-contiguous tiles are stored [64 rows][64 k]
+// with the 256 x 256 kernel's XOR swizzle and read with ds_read_b128;
+// MN-contiguous tiles [64 k][64 mn] are read with ds_read_b64_tr_b16.
+// Chunks past M, N or K are not loaded and stay 0 (N and K, and M when A
+// is transposed, are multiples of 8, as for the 256 x 256 kernel).
+constexpr uint32_t kSmallChunk = 256;
+constexpr uint32_t kSmallSteps = kSmallChunk / 64;
+constexpr uint64_t kSmallBelowTiles = 32;
+
+template <uint32_t Tile, bool TransposeLeft, bool TransposeRight, int Epi>
+__global__ __launch_bounds__(256) void gemm_f16_small_kernel(
+    uint16_t* out, const uint16_t* __restrict__ left, const uint16_t* __restrict__ right,
+    uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride,
+    uint32_t tiles_n, const uint16_t* addend, uint64_t addend_batch_stride,
+    uint32_t addend_row_stride) {
+  constexpr uint32_t kWT = Tile / 32;                 // 16 x 16 tiles per wave and dimension
+  constexpr uint32_t kStepBytes = Tile * 64 * 2;      // one operand, one 64-k step
+  constexpr uint32_t kMnRow = Tile * 2;               // bytes of an MN-contiguous k row
+  constexpr uint32_t kMnChunks = Tile / 8;            // 16-byte chunks of such a row
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kSmallSteps][kStepBytes];
+  constexpr bool kAK = !TransposeLeft;   // A rows (m) K-contiguous
+  constexpr bool kBK_ = TransposeRight;  // B^T rows (n) K-contiguous
+  const uint64_t batch = blockIdx.y;
+  const uint16_t* A = left + batch * left_batch_stride;
+  const uint16_t* B = right + batch * right_batch_stride;
+  uint16_t* C = out + batch * (uint64_t)M * N;
+  const uint32_t m0 = blockIdx.x / tiles_n * Tile, n0 = blockIdx.x % tiles_n * Tile;
+  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const uint32_t wm = (wave / 2) * (Tile / 2), wn = (wave % 2) * (Tile / 2);
+  const uint32_t r16 = lane % 16, g4 = lane / 16;
+
+  // Chunk q = threadIdx.x + 256 i of an operand's 4 steps: step q / (steps'
+  // chunks), then (row, k chunk) for a K-contiguous tile (8 chunks a row) or
+  // (k row, mn chunk) for an MN-contiguous one (Tile / 8 chunks a row).
+  constexpr uint32_t kStepChunks = kStepBytes / 16;
+  constexpr uint32_t kPer = kSmallSteps * kStepChunks / 256;
+  u32x4 ra[kPer], rb[kPer];
+  auto load_operand = [&]<bool KContig>(const uint16_t* X, uint32_t mn0, uint32_t mn_limit,
+                                        uint32_t ld, uint32_t k0, u32x4* r) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = threadIdx.x + 256 * i, step = q / kStepChunks, w = q % kStepChunks;
+      const uint32_t per_row = KContig ? 8 : kMnChunks;
+      const uint32_t major = w / per_row, minor = w % per_row * 8;
+      const uint32_t k = KContig ? k0 + step * 64 + minor : k0 + step * 64 + major;
+      const uint32_t mn = KContig ? mn0 + major : mn0 + minor;
+      const bool ok = k < K && mn < mn_limit;
+      r[i] = ok ? load16(X + (KContig ? (uint64_t)mn * ld + k : (uint64_t)k * ld + mn))
+                : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_operand = [&]<bool KContig>(uint8_t (*stage)[kStepBytes], const u32x4* r) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t q = threadIdx.x + 256 * i, step = q / kStepChunks, w = q % kStepChunks;
+      const uint32_t per_row = KContig ? 8 : kMnChunks;
+      const uint32_t major = w / per_row, chunk = w % per_row;
+      const uint32_t off = KContig ? kc_off<64>(major, chunk) : major * kMnRow + chunk * 16;
+      *reinterpret_cast<u32x4*>(stage[step] + off) = r[i];
+    }
+  };
+  auto load_chunk = [&](uint32_t k0) __attribute__((always_inline)) {
+    load_operand.template operator()<kAK>(A, m0, M, kAK ? K : M, k0, ra);
+    load_operand.template operator()<kBK_>(B, n0, N, kBK_ ? K : N, k0, rb);
+  };
+  auto store_chunk = [&]() __attribute__((always_inline)) {
+    store_operand.template operator()<kAK>(lds[0], ra);
+    store_operand.template operator()<kBK_>(lds[1], rb);
+  };
+  // Fragment of 16 rows (m or n) w0 + 16 t + .., k 32 ss + 8 (lane / 16) ..+7.
+  auto frag = [&]<bool KContig>(const uint8_t* tile, uint32_t w0, uint32_t t, uint32_t ss) __attribute__((always_inline)) {
+    if constexpr (KContig) {
+      const uint32_t row = w0 + 16 * t + r16;
+      return __builtin_bit_cast(
+          half8_t, *reinterpret_cast<const u32x4*>(tile + kc_off<64>(row, 4 * ss + g4)));
+    } else {
+      // 16-lane group g reads k rows 32 ss + 8 g + {0..3} (then +4): lane s
+      // addresses k row + s / 4, columns w0 + 16 t + 4 (s % 4) .. +3.
+      const uint32_t k = 32 * ss + 8 * g4 + r16 / 4;
+      const uint32_t a = k * kMnRow + (w0 + 16 * t + 4 * (r16 % 4)) * 2;
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a));
+      const short4_t hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(tile + a + 4 * kMnRow));
+      return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+
+  float4_t acc[kWT][kWT];
+#pragma unroll
+  for (uint32_t i = 0; i < kWT; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < kWT; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t chunks = (K + kSmallChunk - 1) / kSmallChunk;
+  load_chunk(0);
+  store_chunk();
+  __syncthreads();
+  for (uint32_t c = 0; c < chunks; ++c) {
+    if (c + 1 < chunks) load_chunk((c + 1) * kSmallChunk);
+#pragma unroll
+    for (uint32_t step = 0; step < kSmallSteps; ++step)
+#pragma unroll
+      for (uint32_t ss = 0; ss < 2; ++ss) {
+        half8_t fa[kWT], fb[kWT];
+#pragma unroll
+        for (uint32_t t = 0; t < kWT; ++t) {
+          fa[t] = frag.template operator()<kAK>(lds[0][step], wm, t, ss);
+          fb[t] = frag.template operator()<kBK_>(lds[1][step], wn, t, ss);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kWT; ++i)
+#pragma unroll
+          for (uint32_t j = 0; j < kWT; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+      }
+    if (c + 1 < chunks) {
+      __syncthreads();  // every wave is done reading the stages
+      store_chunk();
+      __syncthreads();
+    }
+  }
+  // acc[i][j][e] = C[m0 + wm + 16 i + lane % 16][n0 + wn + 16 j + 4 (lane / 16) + e]
+#pragma unroll
+  for (uint32_t i = 0; i < kWT; ++i) {
+    const uint32_t m = m0 + wm + 16 * i + r16;
+    if (m >= M) continue;
+#pragma unroll
+    for (uint32_t j = 0; j < kWT; ++j) {
+      const uint32_t n = n0 + wn + 16 * j + 4 * g4;
+      if (n >= N) continue;  // N % 8 == 0: a lane's 4 columns are all in or all out
+      half4_t h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = epilogue<Epi>(acc[i][j][e]);
+      if constexpr (Epi == kEpiAdd) {
+        const half4_t d = *reinterpret_cast<const half4_t*>(
+            addend + batch * addend_batch_stride + (uint64_t)m * addend_row_stride + n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = add_f16(h[e], d[e]);
+      }
+      *reinterpret_cast<half4_t*>(C + (uint64_t)m * N + n) = h;
+    }
+  }
+}
+
+// 64 x 64 tiles, or 32 x 32 when there are fewer 64 x 64 tiles than a
+// quarter of the CUs (256^3: 64 workgroups instead of 16).
+template <int Epi>
+int launch_small(hipStream_t stream, const GemmArgs& a) {
+  const uint64_t tiles64 = (uint64_t)((a.rows + 63) / 64) * ((a.columns + 63) / 64);
+  const uint32_t tile = tiles64 * a.batches < 64 ? 32 : 64;
+  const uint32_t tiles_m = (a.rows + tile - 1) / tile;
+  const uint32_t tiles_n = (a.columns + tile - 1) / tile;
+  const dim3 grid(tiles_m * tiles_n, a.batches);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, (uint16_t*)a.out,
+                       (const uint16_t*)a.left, (const uint16_t*)a.right, a.rows, a.columns,
+                       a.inner, a.left_batch_stride, a.right_batch_stride, tiles_n,
+                       (const uint16_t*)a.addend, a.addend_batch_stride, a.addend_row_stride);
+  };
+  const bool tl = a.transpose_left, tr = a.transpose_right;
+  if (tile == 32) {
+    if (!tl && !tr) go(gemm_f16_small_kernel<32, false, false, Epi>);
+    else if (!tl) go(gemm_f16_small_kernel<32, false, true, Epi>);
+    else if (!tr) go(gemm_f16_small_kernel<32, true, false, Epi>);
+    else go(gemm_f16_small_kernel<32, true, true, Epi>);
+  } else {
+    if (!tl && !tr) go(gemm_f16_small_kernel<64, false, false, Epi>);
+    else if (!tl) go(gemm_f16_small_kernel<64, false, true, Epi>);
+    else if (!tr) go(gemm_f16_small_kernel<64, true, false, Epi>);
+    else go(gemm_f16_small_kernel<64, true, true, Epi>);
+  }
+  return hip_status(hipGetLastError());
+}
+
 template <bool TL, bool TR, int Epi, bool Split>
 int launch_fast(hipStream_t stream, const GemmArgs& a, uint32_t splits, uint32_t k_chunk) {
   const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
@@ -633,6 +815,17 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
   // Any M and N on the fast kernel: rows past the edge read as 0 and are not
   // stored.
   if (fast_ok(a)) {
+    // Fewer 256 x 256 tiles than kSmallBelowTiles: the small-tile kernel
+    // (measured: 256^3 10.7 -> 5.3 us a launch, 1024^3 22 -> 9.6, but
+    // 2048^3 with 64 tiles 40 -> 47).
+    const uint64_t tiles = (uint64_t)((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
+    if (tiles * a.batches < kSmallBelowTiles) {
+      switch (epilogue_of(a)) {
+        case kEpiGelu: return launch_small<kEpiGelu>(stream, a);
+        case kEpiAdd: return launch_small<kEpiAdd>(stream, a);
+        default: return launch_small<kEpiPlain>(stream, a);
+      }
+    }
     switch (epilogue_of(a)) {
       case kEpiGelu: return dispatch_fast<kEpiGelu, false>(stream, a, 1, a.inner);
       case kEpiAdd: return dispatch_fast<kEpiAdd, false>(stream, a, 1, a.inner);
