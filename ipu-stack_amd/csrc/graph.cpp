@@ -606,14 +606,16 @@ int build_error(const std::string& message) {
 }
 
 // Split-K count for an fp16 GEMM on the 256 x 256 kernel: min(16, K / 1024,
-// 64 / tiles), i.e. only for outputs of at most 32 tiles and K >= 2048, with
-// every split keeping >= 1024 k and about 64 workgroups in all (measured:
-// 729 x 1152 x 4304 115 -> 45 us at 4 splits, 256 x 256 x 8192 132 -> 32 us
-// at 8, 1024 x 1024 x 8192 134 -> 59 us at 4; more splits lose to the fp32
-// partials' traffic).  Returns 1 (no split) when the shape is outside the
-// fast kernel's reach.
+// 64 / tiles), i.e. only for outputs of at most 32 tiles and K >= 6144, with
+// every split keeping >= 1024 k and about 64 workgroups in all.  Below
+// 32 tiles the unsplit launch runs the small-tile kernel, which beats the
+// split up to K ~ 4-6k (measured, us, unsplit against split: 1024 x 1024 x
+// 2048 17 / 31, 729 x 1152 x 4304 33 / 38, 512 x 512 x 4096 28 / 30) and
+// loses beyond (1024 x 1024 x 8192 57 / 49, 256 x 1024 x 16384 103 / 37,
+// 64 x 64 x 40000 151 / 51; 256 x 256 x 8192 33 / 32).  Returns 1 (no split)
+// when the shape is outside the fast kernel's reach.
 uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K, uint64_t batches, bool tl, bool tr) {
-  if (K < 2048 || K % 8 != 0 || N % 8 != 0 || (tl && M % 8 != 0)) return 1;
+  if (K < 6144 || K % 8 != 0 || N % 8 != 0 || (tl && M % 8 != 0)) return 1;
   const uint64_t a_span = tl ? (uint64_t)K * M * 2 : 256ull * K * 2;
   const uint64_t b_span = tr ? 256ull * K * 2 : (uint64_t)K * N * 2;
   if (a_span >= (1ull << 31) || b_span >= (1ull << 31)) return 1;

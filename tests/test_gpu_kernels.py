@@ -664,6 +664,10 @@ def test_flat_add_rejects_strides_that_do_not_divide(ipus, ctx):
 # GEMM K tail: reads past K stay inside the operand
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("M,N,K,tl,tr", [
+    # 256 x 256 kernel (>= 32 output tiles), K % 64 = 8 in every layout
+    (2048, 1032, 200, 0, 0), (2000, 1032, 4296, 0, 1), (1032, 2048, 72, 1, 0),
+    (1032, 2000, 136, 1, 1),
+    # small-tile kernel
     (729, 1152, 4304, 0, 0),   # NN, K % 64 = 16: row-major B is MN-contiguous
     (264, 520, 72, 1, 0),      # A^T and B both MN-contiguous, K % 64 = 8
     (264, 520, 72, 0, 1),      # both K-contiguous
@@ -703,7 +707,10 @@ def _addend_layout(kind, batches, M, N):
     (256, 256, 256, 0, 0, 1, "full"), (300, 264, 72, 0, 0, 1, "full"),
     (264, 520, 200, 1, 0, 2, "full"), (130, 264, 128, 0, 1, 3, "matrix"),
     (128, 512, 256, 1, 1, 1, "rows"), (100, 60, 40, 0, 0, 2, "full"),
-    (17, 19, 72, 0, 1, 1, "rows"), (1024, 1024, 1024, 0, 0, 1, "full")])
+    (17, 19, 72, 0, 1, 1, "rows"), (1024, 1024, 1024, 0, 0, 1, "full"),
+    # 256 x 256 kernel (>= 32 output tiles)
+    (2048, 1024, 256, 0, 0, 1, "full"), (2000, 1032, 72, 1, 0, 1, "rows"),
+    (1024, 1024, 128, 0, 1, 2, "matrix")])
 def test_gemm_f16_accumulate_bit_identical_to_gemm_then_add(ipus, ctx, M, N, K, tl, tr,
                                                             batches, kind):
     a = synth(ipus, batches * M * K, 51, 1)

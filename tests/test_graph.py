@@ -157,21 +157,22 @@ def test_build_package_mlp_plan(ipus):
 
 
 def test_split_k_plan_for_few_tiles_and_long_k(ipus):
-    """The reference's SigLIP MLP at one image (729 tokens): its second GEMM has
-    3 x 5 output tiles and K = 4304, so it is split over K into fp32 partials
-    (an arena value) and summed; GELU after the first GEMM fuses into that
-    GEMM, a GELU after a split GEMM into the reduction."""
+    """The reference's SigLIP MLP shape at one image (729 tokens) with a
+    doubled hidden width: its second GEMM has 3 x 5 output tiles and K =
+    8608, so it is split over K into fp32 partials (an arena value) and
+    summed; GELU after the first GEMM fuses into that GEMM, a GELU after a
+    split GEMM into the reduction."""
     g = ipus.ComputeGraph()
     x = g.host_input("x", [729, 1152])
-    w1 = g.parameter("w1", [1152, 4304])
-    w2 = g.parameter("w2", [4304, 1152])
+    w1 = g.parameter("w1", [1152, 8608])
+    w2 = g.parameter("w2", [8608, 1152])
     g.set_outputs([g.gelu(g.gemm(g.gelu(g.gemm(x, w1)), w2))])
     pkg = ipus.build_package(g)
     syms = [s[0] for s in pkg.steps]
     assert syms == ["ipu_stack_gemm_f16_gelu", "ipu_stack_gemm_f16_split",
                     "ipu_stack_reduce_splits_f16"]
     split, reduce = pkg.steps[1][2], pkg.steps[2][2]
-    assert split[:4] == (1, 729, 1152, 4304)
+    assert split[:4] == (1, 729, 1152, 8608)
     splits = split[8]
     assert 2 <= splits <= 16
     assert reduce == (splits, 729 * 1152, 1)  # GELU fused into the reduction
@@ -199,14 +200,15 @@ def _single_gemm_package(ipus, m, n, k, config=None):
 @pytest.mark.parametrize("m,n,k,splits", [
     # tiles = ceil(m/256) * ceil(n/256); splits = ceil(k / c) with
     # c = 64 * ceil(ceil(k / want) / 64), want = min(16, k // 1024, 64 // tiles).
-    (729, 1152, 4304, 4),   # 15 tiles: want 4, c = 1088
+    (729, 1152, 8608, 4),   # 15 tiles: want 4, c = 2176
+    (729, 1152, 4304, 1),   # k < 6144: the small-tile kernel, one launch
     (256, 256, 8192, 8),    # 1 tile: want 8, c = 1024
     (1024, 1024, 8192, 4),  # 16 tiles: want 4, c = 2048
     (64, 64, 40000, 16),    # 1 tile: want 16, c = 2560, 15.6 -> 16
     (2048, 2048, 8192, 1),  # 64 tiles: want 1, one launch
-    (729, 1152, 1960, 1),   # k < 2048: one launch
-    (729, 1152, 4300, 1),   # k not a multiple of 8: one launch
-    (729, 1150, 4304, 1),   # n not a multiple of 8: one launch
+    (729, 1152, 1960, 1),   # k < 6144: one launch
+    (729, 1152, 8604, 1),   # k not a multiple of 8: one launch
+    (729, 1150, 8608, 1),   # n not a multiple of 8: one launch
 ])
 def test_split_k_plan_counts(ipus, m, n, k, splits):
     """The planner's split count for few-tile, long-K GEMMs, and the arena
@@ -314,7 +316,7 @@ def test_gemm_add_fusion_plans(ipus):
         s[0] for s in steps(plain, ipus.PackageConfig(compute_precision="f32"))]
     # a split-K GEMM fuses into its reduction
     def split(g):
-        y = g.gemm(g.host_input("x", [729, 4304]), g.parameter("w", [4304, 1152]))
+        y = g.gemm(g.host_input("x", [729, 8608]), g.parameter("w", [8608, 1152]))
         return g.add(g.host_input("r", [729, 1152]), y)
     (s0, _), (s1, sc) = steps(split)
     assert s0 == "ipu_stack_gemm_f16_split" and s1 == "ipu_stack_reduce_splits_accumulate_f16"
