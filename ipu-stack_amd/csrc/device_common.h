@@ -75,7 +75,13 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float t = x * x;
   const float v = x * fmaf(t, 0.044715f, 1.0f);  // x + 0.044715 x^3
   const float e = __builtin_amdgcn_exp2f(v * kA);
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
+  // The product is rounded to fp32 here: left visible, the compiler fuses
+  // it with a caller's conversion to fp16 (v_fma_mix, one rounding instead
+  // of two) in some kernels and not in others, and the GEMM epilogue must
+  // produce the GELU kernel's bits.
+  float y = x * __builtin_amdgcn_rcpf(1.0f + e);
+  asm("" : "+v"(y));
+  return y;
 }
 
 }  // namespace ipus

@@ -451,55 +451,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_256_kernel(
   }
 }
 
-// General fp16 GEMM: 64 x 64 tile, 4 waves of one 32 x 32 MFMA tile each,
-// K step 16, bounds-checked scalar loads.  Any shape, transposes, batches.
-__global__ __launch_bounds__(256) void gemm_f16_general_kernel(
-    uint16_t* out, const uint16_t* __restrict__ left, const uint16_t* __restrict__ right,
-    uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr, uint64_t left_batch_stride,
-    uint64_t right_batch_stride, uint32_t tiles_n, int epi, const uint16_t* addend,
-    uint64_t addend_batch_stride, uint32_t addend_row_stride) {
-  __shared__ __attribute__((aligned(16))) half_t As[64][24];
-  __shared__ __attribute__((aligned(16))) half_t Bs[64][24];
-  const uint64_t batch = blockIdx.y;
-  const uint16_t* A = left + batch * left_batch_stride;
-  const uint16_t* B = right + batch * right_batch_stride;
-  uint16_t* C = out + batch * (uint64_t)M * N;
-  const uint32_t m0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
-  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t wm = (wave / 2) * 32, wn = (wave % 2) * 32;
-  const uint64_t lda = tl ? M : K, ldb = tr ? K : N;
-  float16_t acc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  for (uint32_t k0 = 0; k0 < K; k0 += 16) {
-    for (uint32_t idx = threadIdx.x; idx < 64 * 16; idx += 256) {
-      const uint32_t r = idx / 16, k = idx % 16;
-      const uint32_t m = m0 + r, n = n0 + r, kk = k0 + k;
-      uint16_t a = 0, b = 0;
-      if (m < M && kk < K) a = tl ? A[(uint64_t)kk * lda + m] : A[(uint64_t)m * lda + kk];
-      if (n < N && kk < K) b = tr ? B[(uint64_t)n * ldb + kk] : B[(uint64_t)kk * ldb + n];
-      As[r][k] = __builtin_bit_cast(half_t, a);
-      Bs[r][k] = __builtin_bit_cast(half_t, b);
-    }
-    __syncthreads();
-    const half8_t fa = *reinterpret_cast<const half8_t*>(&As[wm + lane % 32][(lane / 32) * 8]);
-    const half8_t fb = *reinterpret_cast<const half8_t*>(&Bs[wn + lane % 32][(lane / 32) * 8]);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb, fa, acc, 0, 0, 0);
-    __syncthreads();
-  }
-  const uint32_t m = m0 + wm + lane % 32;
-  if (m >= M) return;
-  const uint16_t* D = addend + batch * addend_batch_stride + (uint64_t)m * addend_row_stride;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t n = n0 + wn + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-    if (n >= N) continue;
-    half_t h = epi == kEpiGelu ? epilogue<kEpiGelu>(acc[r]) : epilogue<kEpiPlain>(acc[r]);
-    if (epi == kEpiAdd) h = add_f16(h, __builtin_bit_cast(half_t, D[n]));
-    C[(uint64_t)m * N + n] = __builtin_bit_cast(uint16_t, h);
-  }
-}
-
 // Small fp16 GEMM: 64 x 64 or 32 x 32 output tiles, for shapes with fewer
 // 256 x 256 tiles than kSmallBelowTiles, which would keep few of the 256
 // CUs busy (configs[0]'s 256^3 is a single such tile).  256 threads = 4
@@ -512,13 +463,17 @@ __global__ __launch_bounds__(256) void gemm_f16_general_kernel(
 // takes one memory round trip.  K-contiguous tiles are stored [64 rows][64 k]
 // with the 256 x 256 kernel's XOR swizzle and read with ds_read_b128;
 // MN-contiguous tiles [64 k][64 mn] are read with ds_read_b64_tr_b16.
-// Chunks past M, N or K are not loaded and stay 0 (N and K, and M when A
-// is transposed, are multiples of 8, as for the 256 x 256 kernel).
+// Chunks past M, N or K are not loaded and stay 0.  Vec = 8: N and K, and
+// M when A is transposed, are multiples of 8 and the operands 16-byte
+// aligned, as for the 256 x 256 kernel.  Vec = 4 or 1 (any other shape or
+// alignment, where the 256 x 256 kernel cannot run): each 16-byte LDS chunk
+// is gathered from 8-byte or 2-byte loads, elements past M, N or K are 0,
+// and the epilogue stores element by element.
 constexpr uint32_t kSmallChunk = 256;
 constexpr uint32_t kSmallSteps = kSmallChunk / 64;
 constexpr uint64_t kSmallBelowTiles = 32;
 
-template <uint32_t Tile, bool TransposeLeft, bool TransposeRight, int Epi>
+template <uint32_t Tile, bool TransposeLeft, bool TransposeRight, int Epi, int Vec = 8>
 __global__ __launch_bounds__(256) void gemm_f16_small_kernel(
     uint16_t* out, const uint16_t* __restrict__ left, const uint16_t* __restrict__ right,
     uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride,
@@ -555,9 +510,32 @@ __global__ __launch_bounds__(256) void gemm_f16_small_kernel(
       const uint32_t major = w / per_row, minor = w % per_row * 8;
       const uint32_t k = KContig ? k0 + step * 64 + minor : k0 + step * 64 + major;
       const uint32_t mn = KContig ? mn0 + major : mn0 + minor;
-      const bool ok = k < K && mn < mn_limit;
-      r[i] = ok ? load16(X + (KContig ? (uint64_t)mn * ld + k : (uint64_t)k * ld + mn))
-                : u32x4{0, 0, 0, 0};
+      const uint16_t* p = X + (KContig ? (uint64_t)mn * ld + k : (uint64_t)k * ld + mn);
+      if constexpr (Vec == 8) {
+        const bool ok = k < K && mn < mn_limit;
+        r[i] = ok ? load16(p) : u32x4{0, 0, 0, 0};
+      } else {
+        // The chunk's 8 elements run along the contiguous axis (k or mn);
+        // groups of Vec are wholly in or out, as Vec divides that extent.
+        const bool row_ok = KContig ? mn < mn_limit : k < K;
+        const uint32_t c0 = KContig ? k : mn, c_limit = KContig ? K : mn_limit;
+        uint16_t e[8];
+#pragma unroll
+        for (uint32_t g = 0; g < 8; g += Vec) {
+          const bool ok = row_ok && c0 + g < c_limit;
+          if constexpr (Vec == 4) {
+            const u32x2 v = ok ? *reinterpret_cast<const u32x2*>(p + g) : u32x2{0, 0};
+            e[g] = (uint16_t)v[0];
+            e[g + 1] = (uint16_t)(v[0] >> 16);
+            e[g + 2] = (uint16_t)v[1];
+            e[g + 3] = (uint16_t)(v[1] >> 16);
+          } else {
+            e[g] = ok ? p[g] : (uint16_t)0;
+          }
+        }
+        r[i] = u32x4{e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                     e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16};
+      }
     }
   };
   auto store_operand = [&]<bool KContig>(uint8_t (*stage)[kStepBytes], const u32x4* r) __attribute__((always_inline)) {
@@ -637,24 +615,37 @@ __global__ __launch_bounds__(256) void gemm_f16_small_kernel(
 #pragma unroll
     for (uint32_t j = 0; j < kWT; ++j) {
       const uint32_t n = n0 + wn + 16 * j + 4 * g4;
-      if (n >= N) continue;  // N % 8 == 0: a lane's 4 columns are all in or all out
+      if (n >= N) continue;
       half4_t h;
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = epilogue<Epi>(acc[i][j][e]);
-      if constexpr (Epi == kEpiAdd) {
-        const half4_t d = *reinterpret_cast<const half4_t*>(
-            addend + batch * addend_batch_stride + (uint64_t)m * addend_row_stride + n);
+      if constexpr (Vec == 8) {
+        // N % 8 == 0: a lane's 4 columns are all in or all out.
+        if constexpr (Epi == kEpiAdd) {
+          const half4_t d = *reinterpret_cast<const half4_t*>(
+              addend + batch * addend_batch_stride + (uint64_t)m * addend_row_stride + n);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = add_f16(h[e], d[e]);
+          for (int e = 0; e < 4; ++e) h[e] = add_f16(h[e], d[e]);
+        }
+        *reinterpret_cast<half4_t*>(C + (uint64_t)m * N + n) = h;
+      } else {
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+          if (n + e >= N) break;
+          half_t v = h[e];
+          if constexpr (Epi == kEpiAdd)
+            v = add_f16(v, __builtin_bit_cast(half_t, addend[batch * addend_batch_stride +
+                                                             (uint64_t)m * addend_row_stride + n + e]));
+          C[(uint64_t)m * N + n + e] = __builtin_bit_cast(uint16_t, v);
+        }
       }
-      *reinterpret_cast<half4_t*>(C + (uint64_t)m * N + n) = h;
     }
   }
 }
 
 // 64 x 64 tiles, or 32 x 32 when there are fewer 64 x 64 tiles than a
 // quarter of the CUs (256^3: 64 workgroups instead of 16).
-template <int Epi>
+template <int Epi, int Vec = 8>
 int launch_small(hipStream_t stream, const GemmArgs& a) {
   const uint64_t tiles64 = (uint64_t)((a.rows + 63) / 64) * ((a.columns + 63) / 64);
   const uint32_t tile = tiles64 * a.batches < 64 ? 32 : 64;
@@ -669,17 +660,45 @@ int launch_small(hipStream_t stream, const GemmArgs& a) {
   };
   const bool tl = a.transpose_left, tr = a.transpose_right;
   if (tile == 32) {
-    if (!tl && !tr) go(gemm_f16_small_kernel<32, false, false, Epi>);
-    else if (!tl) go(gemm_f16_small_kernel<32, false, true, Epi>);
-    else if (!tr) go(gemm_f16_small_kernel<32, true, false, Epi>);
-    else go(gemm_f16_small_kernel<32, true, true, Epi>);
+    if (!tl && !tr) go(gemm_f16_small_kernel<32, false, false, Epi, Vec>);
+    else if (!tl) go(gemm_f16_small_kernel<32, false, true, Epi, Vec>);
+    else if (!tr) go(gemm_f16_small_kernel<32, true, false, Epi, Vec>);
+    else go(gemm_f16_small_kernel<32, true, true, Epi, Vec>);
   } else {
-    if (!tl && !tr) go(gemm_f16_small_kernel<64, false, false, Epi>);
-    else if (!tl) go(gemm_f16_small_kernel<64, false, true, Epi>);
-    else if (!tr) go(gemm_f16_small_kernel<64, true, false, Epi>);
-    else go(gemm_f16_small_kernel<64, true, true, Epi>);
+    if (!tl && !tr) go(gemm_f16_small_kernel<64, false, false, Epi, Vec>);
+    else if (!tl) go(gemm_f16_small_kernel<64, false, true, Epi, Vec>);
+    else if (!tr) go(gemm_f16_small_kernel<64, true, false, Epi, Vec>);
+    else go(gemm_f16_small_kernel<64, true, true, Epi, Vec>);
   }
   return hip_status(hipGetLastError());
+}
+
+// Elements per global load (8, 4 or 1) that every operand row, batch and
+// base address allows, and 8 only where the addend and output allow the
+// 16-byte epilogue too.
+uint32_t small_vec(const GemmArgs& a) {
+  auto fits = [&](uint32_t v) {
+    const uint32_t lda = a.transpose_left ? a.rows : a.inner;
+    const uint32_t ldb = a.transpose_right ? a.inner : a.columns;
+    bool ok = lda % v == 0 && ldb % v == 0 && (uintptr_t)a.left % (2 * v) == 0 &&
+              (uintptr_t)a.right % (2 * v) == 0 && a.left_batch_stride % v == 0 &&
+              a.right_batch_stride % v == 0;
+    if (v == 8)
+      ok = ok && a.inner % 8 == 0 && a.columns % 8 == 0 && (uintptr_t)a.out % 16 == 0 &&
+           (!a.addend || ((uintptr_t)a.addend % 16 == 0 && a.addend_batch_stride % 8 == 0 &&
+                          a.addend_row_stride % 8 == 0));
+    return ok;
+  };
+  return fits(8) ? 8u : fits(4) ? 4u : 1u;
+}
+
+template <int Epi>
+int launch_small_any(hipStream_t stream, const GemmArgs& a) {
+  switch (small_vec(a)) {
+    case 8: return launch_small<Epi, 8>(stream, a);
+    case 4: return launch_small<Epi, 4>(stream, a);
+    default: return launch_small<Epi, 1>(stream, a);
+  }
 }
 
 template <bool TL, bool TR, int Epi, bool Split>
@@ -832,13 +851,14 @@ int launch_gemm_f16(hipStream_t stream, const GemmArgs& a) {
       default: return dispatch_fast<kEpiPlain, false>(stream, a, 1, a.inner);
     }
   }
-  const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
-  hipLaunchKernelGGL(gemm_f16_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
-                     stream, (uint16_t*)a.out, (const uint16_t*)a.left, (const uint16_t*)a.right,
-                     a.rows, a.columns, a.inner, a.transpose_left, a.transpose_right,
-                     a.left_batch_stride, a.right_batch_stride, tiles_n, epilogue_of(a),
-                     (const uint16_t*)a.addend, a.addend_batch_stride, a.addend_row_stride);
-  return hip_status(hipGetLastError());
+  // Any other shape or alignment (or operands past the 256 x 256 kernel's
+  // 31-bit buffer ranges): the small-tile kernel with the widest loads the
+  // operands allow.
+  switch (epilogue_of(a)) {
+    case kEpiGelu: return launch_small_any<kEpiGelu>(stream, a);
+    case kEpiAdd: return launch_small_any<kEpiAdd>(stream, a);
+    default: return launch_small_any<kEpiPlain>(stream, a);
+  }
 }
 
 // ---------------------------------------------------------------------------

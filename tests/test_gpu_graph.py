@@ -129,7 +129,8 @@ def test_split_k_rejects_empty_splits(ipus, ctx):
 
 
 @pytest.mark.parametrize("M,N,K,tl,tr", [(256, 512, 128, 0, 0), (512, 256, 192, 1, 1),
-                                         (100, 60, 40, 0, 0), (64, 96, 48, 0, 1)])
+                                         (100, 60, 40, 0, 0), (64, 96, 48, 0, 1),
+                                         (66, 68, 129, 1, 0), (130, 132, 260, 0, 0)])
 def test_gemm_gelu_fusion_bit_exact(ipus, ctx, M, N, K, tl, tr):
     a = synth(ipus, M * K, 32, 1)
     b = synth(ipus, K * N, 32, 2, scale=0.2)

@@ -261,6 +261,55 @@ def test_gemm_f16_ragged_tiles(ipus, oracle, ctx, tl, tr, M, N, K):
     assert fp16_close(got, want, FP16_TOL)
 
 
+@pytest.mark.parametrize("tl", [False, True])
+@pytest.mark.parametrize("tr", [False, True])
+@pytest.mark.parametrize("M,N,K", [(65, 67, 129), (130, 132, 260), (300, 261, 517), (1, 3, 5),
+                                   (68, 20, 12)])
+def test_gemm_f16_unaligned_shapes(ipus, oracle, ctx, tl, tr, M, N, K):
+    """Row pitches that are not multiples of 8 elements: the small-tile
+    kernel gathers its LDS chunks from 8-byte loads (pitches that are
+    multiples of 4) or 2-byte loads, and stores element by element."""
+    got, want = gemm_case(ipus, oracle, ctx, M, N, K, tl, tr)
+    assert fp16_close(got, want, FP16_TOL)
+
+
+def test_gemm_f16_unaligned_large(ipus, oracle, ctx):
+    # several 256-deep K chunks and a partial last one, 16 x 16 output tiles
+    got, want = gemm_case(ipus, oracle, ctx, 1000, 1000, 1001)
+    assert fp16_close(got, want, FP16_TOL)
+
+
+@pytest.mark.parametrize("bl,br", [(True, True), (True, False), (False, True)])
+def test_gemm_f16_unaligned_batched_broadcast(ipus, oracle, ctx, bl, br):
+    got, want = gemm_case(ipus, oracle, ctx, 70, 66, 45, batches=3, bl=bl, br=br)
+    assert fp16_close(got, want, FP16_TOL)
+
+
+@pytest.mark.parametrize("shift_a,shift_b,shift_c", [(2, 0, 0), (0, 2, 0), (0, 0, 2), (8, 8, 8),
+                                                     (4, 12, 6)])
+def test_gemm_f16_misaligned_pointers(ipus, oracle, ctx, shift_a, shift_b, shift_c):
+    """Operands and output at 2-, 4- or 8-byte offsets into their
+    allocations (a shape the 256 x 256 kernel takes when aligned)."""
+    M, N, K = 256, 264, 136
+    a = synth(ipus, M * K, 23, 1)
+    b = synth(ipus, K * N, 23, 2)
+    da = ctx.upload(np.concatenate([np.zeros(8, np.uint16), a]))
+    db = ctx.upload(np.concatenate([np.zeros(8, np.uint16), b]))
+    out = ctx.upload(np.full(M * N + 16, 0x7E00, np.uint16))
+    ctx.launch("ipu_stack_gemm_f16", out.ptr + shift_c,
+               [da.ptr + 16 - shift_a, db.ptr + 16 - shift_b], [1, M, N, K, 0, 0, 0, 0])
+    # the shifted pointers address a and b exactly: read them back the same way
+    raw = out.download(np.uint16)
+    got = raw[shift_c // 2: shift_c // 2 + M * N]
+    assert (raw[:shift_c // 2] == 0x7E00).all() and (raw[shift_c // 2 + M * N:] == 0x7E00).all()
+    ea = np.concatenate([np.zeros(8, np.uint16), a])[(16 - shift_a) // 2:][:M * K]
+    eb = np.concatenate([np.zeros(8, np.uint16), b])[(16 - shift_b) // 2:][:K * N]
+    want = oracle.gemm_f16(ea, eb, M, N, K, False, False)
+    assert fp16_close(oracle.f16_to_f32(got), oracle.f16_to_f32(want), FP16_TOL)
+    for x in (da, db, out):
+        x.free()
+
+
 def test_gemm_f16_ragged_batched(ipus, oracle, ctx):
     got, want = gemm_case(ipus, oracle, ctx, 300, 136, 200, batches=3)
     assert fp16_close(got, want, FP16_TOL)
@@ -672,6 +721,8 @@ def test_flat_add_rejects_strides_that_do_not_divide(ipus, ctx):
     (264, 520, 72, 1, 0),      # A^T and B both MN-contiguous, K % 64 = 8
     (264, 520, 72, 0, 1),      # both K-contiguous
     (130, 264, 200, 1, 1),     # A^T MN-contiguous, B^T K-contiguous
+    # small-tile kernel on pitches that are not multiples of 8 (2- and 8-byte loads)
+    (65, 67, 129, 0, 0), (130, 132, 260, 1, 1), (300, 261, 517, 0, 1), (67, 300, 131, 1, 0),
 ])
 def test_gemm_k_tail_ignores_memory_after_the_operands(ipus, oracle, ctx, M, N, K, tl, tr):
     """Each operand is followed in its own allocation by 64 rows of fp16 NaN:
@@ -710,7 +761,10 @@ def _addend_layout(kind, batches, M, N):
     (17, 19, 72, 0, 1, 1, "rows"), (1024, 1024, 1024, 0, 0, 1, "full"),
     # 256 x 256 kernel (>= 32 output tiles)
     (2048, 1024, 256, 0, 0, 1, "full"), (2000, 1032, 72, 1, 0, 1, "rows"),
-    (1024, 1024, 128, 0, 1, 2, "matrix")])
+    (1024, 1024, 128, 0, 1, 2, "matrix"),
+    # pitches that are not multiples of 8
+    (65, 67, 129, 0, 0, 2, "full"), (130, 132, 260, 1, 0, 1, "matrix"),
+    (66, 41, 77, 0, 1, 1, "rows")])
 def test_gemm_f16_accumulate_bit_identical_to_gemm_then_add(ipus, ctx, M, N, K, tl, tr,
                                                             batches, kind):
     a = synth(ipus, batches * M * K, 51, 1)
