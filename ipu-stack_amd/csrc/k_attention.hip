@@ -554,6 +554,216 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   }
 }
 
+// MFMA attention for the widths the fast kernel does not take: query/key
+// width up to 256 and value width up to 512, equal or not, multiples of 8
+// or not.  256 threads = 4 waves of 16 queries (one 16-query tile each); a
+// workgroup runs 64 queries of one stream (the heaviest causal blocks first)
+// and shares each block of 32 keys through LDS: the K and V tiles of the
+// next block are loaded into registers while the current one computes
+// (16-byte loads, or 2-byte loads when a width is not a multiple of 8; zero
+// past the key rows and the widths), then stored with the fast kernel's XOR
+// swizzles.  S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_f16 with
+// the fast kernel's lane layouts (a lane holds 4 keys of one query per
+// 16-key tile, its probabilities are the output MFMA's operand in place).
+// The running maximum is updated every block and the output rescaled, as in
+// device/flash_attention_online_f16.cpp:68-143.
+namespace wide {
+constexpr uint32_t kKeys = 32;
+constexpr uint32_t kQueries = 64;  // per workgroup
+
+template <uint32_t DMAX, uint32_t DVMAX, bool Vec8>
+__global__ __launch_bounds__(kThreads) void attention_wide_kernel(
+    void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
+    const uint16_t* __restrict__ value, uint32_t query_rows, uint32_t key_rows, uint32_t width,
+    uint32_t value_width, float scale_log2, bool causal, bool out_f16, uint32_t q_heads,
+    uint32_t k_heads, uint32_t v_heads, uint32_t qblocks) {
+  constexpr uint32_t kKRow = DMAX * 2, kVRow = DVMAX * 2;  // LDS row bytes
+  constexpr uint32_t kKS = DMAX / 32, kDT = DVMAX / 16;
+  constexpr uint32_t kKChunks = DMAX / 8, kVChunks = DVMAX / 8;  // 16-byte chunks a row
+  constexpr uint32_t kKPer = kKeys * kKChunks / kThreads, kVPer = kKeys * kVChunks / kThreads;
+  static_assert(kKChunks >= 16 && kVChunks >= 16, "swizzles need 16 chunks a row");
+  __shared__ __attribute__((aligned(16))) uint8_t lk[kKeys * kKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t lv[kKeys * kVRow];
+
+  const uint32_t stream = blockIdx.x / qblocks;
+  const uint32_t qb = qblocks - 1 - blockIdx.x % qblocks;
+  const uint32_t lane = threadIdx.x % kWave, r16 = lane % 16, g4 = lane / 16;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t q0 = qb * kQueries;
+  const uint32_t qi = q0 + wave * 16 + r16;  // this lane's query
+  const uint32_t q_pitch = q_heads * width, k_pitch = k_heads * width;
+  const uint32_t v_pitch = v_heads * value_width;
+  const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * width;
+  const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_pitch + (stream % k_heads) * width;
+  const uint16_t* V =
+      value + (uint64_t)(stream / v_heads) * key_rows * v_pitch + (stream % v_heads) * value_width;
+  const uint32_t nks = (width + 31) / 32, ndt = (value_width + 15) / 16;
+
+  // Elements c .. c + 7 of a row of `limit` elements (zero past it).
+  auto load8 = [&](const uint16_t* row, uint32_t c, uint32_t limit) __attribute__((always_inline)) {
+    if constexpr (Vec8) {
+      return c < limit ? load16(row + c) : u32x4{0, 0, 0, 0};  // limit % 8 == 0
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t lo = c + 2 * i < limit ? row[c + 2 * i] : 0u;
+        const uint32_t hi = c + 2 * i + 1 < limit ? row[c + 2 * i + 1] : 0u;
+        w[i] = lo | hi << 16;
+      }
+      return u32x4{w[0], w[1], w[2], w[3]};
+    }
+  };
+
+  // Q fragment k step ks: Q[qi][32 ks + 8 (l / 16) .. +7] (rows clamped).
+  half8_t qf[kKS];
+  {
+    const uint32_t q = qi < query_rows ? qi : query_rows - 1;
+#pragma unroll
+    for (uint32_t ks = 0; ks < kKS; ++ks)
+      qf[ks] = __builtin_bit_cast(half8_t, load8(Q + (uint64_t)q * q_pitch, 32 * ks + 8 * g4, width));
+  }
+
+  uint32_t key_end = key_rows;
+  if (causal) {
+    const uint32_t last_q = q0 + kQueries < query_rows ? q0 + kQueries : query_rows;
+    key_end = last_q < key_rows ? last_q : key_rows;
+  }
+  const uint32_t nblocks = (key_end + kKeys - 1) / kKeys;
+
+  // Tile chunk i of this thread: row (i * 256 + t) / chunks, chunk % chunks.
+  u32x4 rk[kKPer], rv[kVPer];
+  auto load_tiles = [&](uint32_t kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t i = 0; i < kKPer; ++i) {
+      const uint32_t c = i * kThreads + threadIdx.x, row = c / kKChunks, ch = c % kKChunks;
+      rk[i] = kb + row < key_rows ? load8(K + (uint64_t)(kb + row) * k_pitch, 8 * ch, width)
+                                  : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kVPer; ++i) {
+      const uint32_t c = i * kThreads + threadIdx.x, row = c / kVChunks, ch = c % kVChunks;
+      rv[i] = kb + row < key_rows ? load8(V + (uint64_t)(kb + row) * v_pitch, 8 * ch, value_width)
+                                  : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tiles = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t i = 0; i < kKPer; ++i) {
+      const uint32_t c = i * kThreads + threadIdx.x, row = c / kKChunks, ch = c % kKChunks;
+      *reinterpret_cast<u32x4*>(lk + row * kKRow + ((ch ^ (row & 15u)) << 4)) = rk[i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kVPer; ++i) {
+      const uint32_t c = i * kThreads + threadIdx.x, row = c / kVChunks, ch = c % kVChunks;
+      *reinterpret_cast<u32x4*>(lv + row * kVRow + ((ch ^ ((row & 7u) << 1)) << 4)) = rv[i];
+    }
+  };
+  const uint32_t kbase = r16 * kKRow + ((g4 ^ (r16 & 15u)) << 4);
+  uint32_t vbase;
+  {
+    const uint32_t row = 4 * g4 + r16 / 4, c1 = (r16 % 4) / 2;
+    vbase = row * kVRow + ((c1 ^ ((row & 7u) << 1)) << 4) + 8 * (r16 % 2);
+  }
+
+  float4_t o[kDT];
+#pragma unroll
+  for (uint32_t dt = 0; dt < kDT; ++dt) o[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  load_tiles(0);
+  for (uint32_t b = 0; b < nblocks; ++b) {
+    const uint32_t kb = b * kKeys;
+    __syncthreads();  // every wave is done with the previous tiles
+    store_tiles();
+    __syncthreads();
+    if (b + 1 < nblocks) load_tiles(kb + kKeys);
+    // Scores: s[kt][e] = key kb + 16 kt + 4 (l / 16) + e of query qi.
+    float4_t s[2];
+#pragma unroll
+    for (uint32_t kt = 0; kt < 2; ++kt) {
+      s[kt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t ks = 0; ks < kKS; ++ks) {
+        if (ks >= nks) break;
+        const half8_t kf = __builtin_bit_cast(
+            half8_t, *reinterpret_cast<const u32x4*>(lk + (kbase ^ (ks << 6)) + 16 * kt * kKRow));
+        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s[kt], 0, 0, 0);
+      }
+    }
+    // Online softmax in log2 units; masked keys are -inf.  A query whose
+    // keys in this block are all masked keeps its reference point (every
+    // query has key 0 in block 0).
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t k = kb + 16 * kt + 4 * g4 + e;
+        const bool ok = k < key_rows && (!causal || k <= qi);
+        s[kt][e] = ok ? s[kt][e] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, s[kt][e]);
+      }
+    mx = max_of_query(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    half8_t pp;
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t e = 0; e < 8; ++e) {
+      const float p = __builtin_amdgcn_exp2f(s[e / 4][e % 4] - m_use);
+      pp[e] = (half_t)p;
+      sum += (float)pp[e];
+    }
+    l_run = l_run * alpha + sum;
+    // Output: o[dt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi].
+#pragma unroll
+    for (uint32_t dt = 0; dt < kDT; ++dt) {
+      if (dt >= ndt) break;
+      const uint8_t* p = lv + (vbase ^ (dt << 5));
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kVRow));
+      const half8_t vf = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pp, o[dt] * alpha, 0, 0, 0);
+    }
+  }
+  const float inv = 1.0f / sum_of_query(l_run);
+  if (qi >= query_rows) return;
+  const uint64_t row = ((uint64_t)stream * query_rows + qi) * value_width;
+#pragma unroll
+  for (uint32_t dt = 0; dt < kDT; ++dt) {
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+      const uint32_t d = dt * 16 + 4 * g4 + e;
+      if (d >= value_width) continue;
+      const float r = o[dt][e] * inv;
+      if (out_f16)
+        ((uint16_t*)out)[row + d] = __builtin_bit_cast(uint16_t, (half_t)r);
+      else
+        ((float*)out)[row + d] = r;
+    }
+  }
+}
+
+template <uint32_t DMAX, uint32_t DVMAX>
+int launch(hipStream_t stream, const AttentionArgs& a, float scale_log2, bool vec8) {
+  const uint32_t qblocks = (a.query_rows + kQueries - 1) / kQueries;
+  const uint64_t blocks = (uint64_t)qblocks * a.streams;
+  if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, a.out,
+                       (const uint16_t*)a.query, (const uint16_t*)a.key, (const uint16_t*)a.value,
+                       a.query_rows, a.key_rows, a.width, a.value_width, scale_log2, a.causal,
+                       a.output_f16, a.heads[0], a.heads[1], a.heads[2], qblocks);
+  };
+  if (vec8) go(attention_wide_kernel<DMAX, DVMAX, true>);
+  else go(attention_wide_kernel<DMAX, DVMAX, false>);
+  return hip_status(hipGetLastError());
+}
+}  // namespace wide
+
 // General attention: one 64-lane block per (stream, query row); any widths.
 // Online softmax over keys one at a time (dot products by wave reduction).
 constexpr uint32_t kGeneralMaxValuePerLane = 8;  // value width <= 512
@@ -654,6 +864,14 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 128) {
     return a.width > 64 ? dispatch_fast<128>(stream, a, scale_log2)
                         : dispatch_fast<64>(stream, a, scale_log2);
+  }
+  // Query/key width up to 256 and value width up to 512: the MFMA kernel for
+  // other widths, in the smallest of its tile classes that holds them.
+  if (a.width <= 256 && a.value_width <= 512) {
+    const bool vec8 = aligned && a.width % 8 == 0 && a.value_width % 8 == 0;
+    if (a.width <= 128 && a.value_width <= 128) return wide::launch<128, 128>(stream, a, scale_log2, vec8);
+    if (a.value_width <= 256) return wide::launch<256, 256>(stream, a, scale_log2, vec8);
+    return wide::launch<256, 512>(stream, a, scale_log2, vec8);
   }
   if (a.value_width > 64 * kGeneralMaxValuePerLane) return IPUS_ERROR_UNAVAILABLE;
   const uint64_t blocks = (uint64_t)a.streams * a.query_rows;

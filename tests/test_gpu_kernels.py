@@ -430,12 +430,26 @@ def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("streams,sq,sk,d,dv", [(2, 50, 70, 160, 160), (1, 33, 45, 64, 96),
                                                 (2, 40, 40, 36, 36), (1, 20, 30, 256, 512),
-                                                (3, 65, 1, 128, 8)])
+                                                (3, 65, 1, 128, 8), (2, 130, 97, 37, 53),
+                                                (1, 200, 260, 200, 72), (2, 64, 64, 136, 136),
+                                                (1, 129, 300, 256, 256), (1, 70, 90, 120, 264),
+                                                (1, 40, 50, 300, 40)])
 def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d, dv):
     """Widths the fast kernel does not take (query/key width above 128, value
-    width different from it, widths not a multiple of 8, value width up to
-    the general kernel's 512) run on the one-row-per-block kernel."""
+    width different from it, widths not a multiple of 8) run on the MFMA
+    kernel for other widths (query/key width up to 256, value width up to
+    512), and query/key widths above 256 on the one-row-per-block kernel."""
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal)
+    assert fp16_close(got, want, FP16_TOL)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal):
+    """Width 136 (the MFMA kernel for other widths) at 16 streams x 2048
+    rows, fp16 output, checked on sampled rows."""
+    rows = [0, 1, 63, 64, 500, 1023, 1024, 2047, 2048 + 5, 16 * 2048 - 1, 7 * 2048 + 1300]
+    got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, 136, 136, causal,
+                               out_f16=True, rows=rows)
     assert fp16_close(got, want, FP16_TOL)
 
 
@@ -535,7 +549,7 @@ def test_attention_causal_first_row_is_first_value(ipus, oracle, ctx):
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("batch,heads,s,d", [(2, 2, 256, 128), (1, 4, 200, 64), (2, 3, 40, 72),
-                                             (1, 16, 130, 72)])
+                                             (1, 16, 130, 72), (2, 2, 100, 136), (1, 3, 70, 44)])
 def test_attention_heads_view_equals_split_copy(ipus, oracle, ctx, causal, batch, heads, s, d):
     """The strided-heads launch on unsplit [batch, rows, heads * d] operands is
     bit-identical to the contiguous launch on split_heads copies (the split is
