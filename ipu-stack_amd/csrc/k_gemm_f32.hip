@@ -2,10 +2,11 @@
 // output: replaces gemm_f32_64_amp (device/gemm_f32_64_amp.S:125-385), whose
 // init mode clears the output and accumulates in fp32 (gemm_f32_64_amp.S:40-56).
 //
-// Fast kernel (16-byte aligned operands whose contiguous axes, and N, are
-// multiples of 4; the Edge
-// instantiation, used off the 128 x 128 x 32 grid, zero-fills loads past M,
-// N or K and stores only rows < M and 4-column chunks < N):
+// One kernel for every shape (16-byte aligned operands whose contiguous
+// axes, and N, are multiples of 4 use 16-byte loads; the kEdge mode, used
+// off the 128 x 128 x 32 grid, zero-fills loads past M, N or K and stores
+// only rows < M and 4-column chunks < N; kScalar covers other shapes and
+// alignments with bounds-checked element loads and stores):
 //   * block tile 128 x 128 x 32, 4 waves in a 2 x 2 grid, each wave 64 x 64
 //     as 2 x 2 MFMA tiles;
 //   * operands staged in LDS k-major ([k][m], [k][n]) so a fragment is 32
@@ -37,12 +38,16 @@ __device__ __forceinline__ uint32_t swz32(uint32_t k, uint32_t x) {
   return k * 512u + ((((x >> 2) ^ ((k >> 2) & 7u)) << 4) | ((x & 3u) << 2));
 }
 
+// Tile modes: kGrid (every tile whole), kEdge (chunks of 4 floats past the
+// extents read as 0 and are not stored; the contiguous axes and N are
+// multiples of 4, so a chunk is wholly inside or outside), kScalar (any
+// shape and alignment: element loads and stores, each bounds-checked).
+enum TileMode : int { kGrid = 0, kEdge = 1, kScalar = 2 };
+
 // Loads a 128 (x) by 32 (k) operand tile.
 // XContig: element (x, k) at base[(k0 + k) * ld + x0 + x]  (stored [K][X])
 // else:    element (x, k) at base[(x0 + x) * ld + k0 + k]  (stored [X][K])
-// Edge: chunks of 4 floats past X (x extent) or K read as 0 (X and K are
-// multiples of 4, so a chunk is wholly inside or outside).
-template <bool XContig, bool Edge>
+template <bool XContig, int Mode>
 __device__ __forceinline__ void load_tile32(const float* __restrict__ base, uint64_t ld,
                                             uint32_t x0, uint32_t k0, u32x4 v[4], uint32_t X,
                                             uint32_t K) {
@@ -52,14 +57,28 @@ __device__ __forceinline__ void load_tile32(const float* __restrict__ base, uint
     const uint32_t k = k0 + t / 32, x = x0 + (t % 32) * 4;
     const float* p = base + (uint64_t)k * ld + x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v[i] = !Edge || (k + 8 * i < K && x < X) ? load16(p + (uint64_t)(8 * i) * ld) : zero;
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (Mode == kScalar) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[i][e] = k + 8 * i < K && x + e < X ? __float_as_uint(p[(uint64_t)(8 * i) * ld + e]) : 0u;
+      } else {
+        v[i] = Mode == kGrid || (k + 8 * i < K && x < X) ? load16(p + (uint64_t)(8 * i) * ld) : zero;
+      }
+    }
   } else {
     const uint32_t x = x0 + (t / 8) * 4, k = k0 + (t % 8) * 4;
     const float* p = base + (uint64_t)x * ld + k;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      v[j] = !Edge || (x + j < X && k < K) ? load16(p + (uint64_t)j * ld) : zero;
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (Mode == kScalar) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[j][e] = x + j < X && k + e < K ? __float_as_uint(p[(uint64_t)j * ld + e]) : 0u;
+      } else {
+        v[j] = Mode == kGrid || (x + j < X && k < K) ? load16(p + (uint64_t)j * ld) : zero;
+      }
+    }
   }
 }
 
@@ -84,7 +103,7 @@ __device__ __forceinline__ float read32(const uint8_t* lds, uint32_t k, uint32_t
   return *reinterpret_cast<const float*>(lds + swz32(k, x));
 }
 
-template <bool TransposeLeft, bool TransposeRight, bool Edge>
+template <bool TransposeLeft, bool TransposeRight, int Mode>
 __global__ __launch_bounds__(kThreads, 3) void gemm_f32_128_kernel(
     float* __restrict__ out, const float* __restrict__ left, const float* __restrict__ right,
     uint32_t M, uint32_t N, uint32_t K, uint64_t left_batch_stride, uint64_t right_batch_stride) {
@@ -124,8 +143,8 @@ __global__ __launch_bounds__(kThreads, 3) void gemm_f32_128_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   u32x4 ra[4], rb[4];
-  load_tile32<kAX, Edge>(A, lda, m0, 0, ra, M, K);
-  load_tile32<kBX, Edge>(B, ldb, n0, 0, rb, N, K);
+  load_tile32<kAX, Mode>(A, lda, m0, 0, ra, M, K);
+  load_tile32<kBX, Mode>(B, ldb, n0, 0, rb, N, K);
   store_tile32<kAX>(smem, ra);
   store_tile32<kBX>(smem + kTileBytes, rb);
   __syncthreads();
@@ -134,8 +153,8 @@ __global__ __launch_bounds__(kThreads, 3) void gemm_f32_128_kernel(
   for (uint32_t kt = 0; kt < ksteps; ++kt) {
     const bool more = kt + 1 < ksteps;
     if (more) {
-      load_tile32<kAX, Edge>(A, lda, m0, (kt + 1) * kBK, ra, M, K);
-      load_tile32<kBX, Edge>(B, ldb, n0, (kt + 1) * kBK, rb, N, K);
+      load_tile32<kAX, Mode>(A, lda, m0, (kt + 1) * kBK, ra, M, K);
+      load_tile32<kBX, Mode>(B, ldb, n0, (kt + 1) * kBK, rb, N, K);
     }
     const uint8_t* la = smem;
     const uint8_t* lb = smem + kTileBytes;
@@ -165,79 +184,40 @@ __global__ __launch_bounds__(kThreads, 3) void gemm_f32_128_kernel(
   const uint32_t col = n0 + wn + 4 * (lane / 32);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    if (Edge && row + 32 * i >= M) continue;
+    if (Mode != kGrid && row + 32 * i >= M) continue;
     float* crow = C + (uint64_t)(row + 32 * i) * N + col;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        if (Edge && col + 32 * j + 8 * g >= N) continue;
-        float4_t v;
+        const uint32_t c = col + 32 * j + 8 * g;
+        if (Mode != kGrid && c >= N) continue;
+        if constexpr (Mode == kScalar) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
-        *reinterpret_cast<float4_t*>(crow + 32 * j + 8 * g) = v;
+          for (int e = 0; e < 4; ++e)
+            if (c + e < N) crow[32 * j + 8 * g + e] = acc[i][j][4 * g + e];
+        } else {
+          float4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+          *reinterpret_cast<float4_t*>(crow + 32 * j + 8 * g) = v;
+        }
       }
   }
 }
 
-// General fp32 GEMM: 64 x 64 tile, 4 waves of one 32 x 32 MFMA tile, K step 8.
-__global__ __launch_bounds__(256) void gemm_f32_general_kernel(
-    float* __restrict__ out, const float* __restrict__ left, const float* __restrict__ right,
-    uint32_t M, uint32_t N, uint32_t K, bool tl, bool tr, uint64_t left_batch_stride,
-    uint64_t right_batch_stride, uint32_t tiles_n) {
-  __shared__ float As[8][64];
-  __shared__ float Bs[8][64];
-  const uint64_t batch = blockIdx.y;
-  const float* A = left + batch * left_batch_stride;
-  const float* B = right + batch * right_batch_stride;
-  float* C = out + batch * (uint64_t)M * N;
-  const uint32_t m0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
-  const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t wm = (wave / 2) * 32, wn = (wave % 2) * 32;
-  const uint64_t lda = tl ? M : K, ldb = tr ? K : N;
-  float16_t acc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  for (uint32_t k0 = 0; k0 < K; k0 += 8) {
-    for (uint32_t idx = threadIdx.x; idx < 64 * 8; idx += 256) {
-      const uint32_t k = idx / 64, x = idx % 64;
-      const uint32_t m = m0 + x, n = n0 + x, kk = k0 + k;
-      float a = 0.0f, b = 0.0f;
-      if (m < M && kk < K) a = tl ? A[(uint64_t)kk * lda + m] : A[(uint64_t)m * lda + kk];
-      if (n < N && kk < K) b = tr ? B[(uint64_t)n * ldb + kk] : B[(uint64_t)kk * ldb + n];
-      As[k][x] = a;
-      Bs[k][x] = b;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t k = 2 * p + lane / 32;
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Bs[k][wn + lane % 32], As[k][wm + lane % 32], acc,
-                                                 0, 0, 0);
-    }
-    __syncthreads();
-  }
-  const uint32_t m = m0 + wm + lane % 32;
-  if (m >= M) return;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t n = n0 + wn + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-    if (n < N) C[(uint64_t)m * N + n] = acc[r];
-  }
-}
-
 template <bool TL, bool TR>
-int launch_fast(hipStream_t stream, const GemmArgs& a) {
+int launch_fast(hipStream_t stream, const GemmArgs& a, bool chunked) {
   const uint32_t tiles = ((a.rows + kBM - 1) / kBM) * ((a.columns + kBN - 1) / kBN);
   const bool grid = a.rows % kBM == 0 && a.columns % kBN == 0 && a.inner % kBK == 0;
-  if (grid)
-    hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR, false>), dim3(tiles, a.batches), dim3(kThreads),
-                       0, stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
-                       a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
-  else
-    hipLaunchKernelGGL((gemm_f32_128_kernel<TL, TR, true>), dim3(tiles, a.batches), dim3(kThreads),
-                       0, stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
-                       a.columns, a.inner, a.left_batch_stride, a.right_batch_stride);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(tiles, a.batches), dim3(kThreads), 0, stream, (float*)a.out,
+                       (const float*)a.left, (const float*)a.right, a.rows, a.columns, a.inner,
+                       a.left_batch_stride, a.right_batch_stride);
+  };
+  if (!chunked) go(gemm_f32_128_kernel<TL, TR, kScalar>);
+  else if (grid) go(gemm_f32_128_kernel<TL, TR, kGrid>);
+  else go(gemm_f32_128_kernel<TL, TR, kEdge>);
   return hip_status(hipGetLastError());
 }
 
@@ -253,18 +233,13 @@ int launch_gemm_f32(hipStream_t stream, const GemmArgs& a) {
   // N always, K for row-major A or transposed B, M for transposed A.
   const bool chunked = a.columns % 4 == 0 && (a.transpose_left ? a.rows % 4 == 0 : a.inner % 4 == 0) &&
                        (!a.transpose_right || a.inner % 4 == 0);
-  if (aligned && chunked && a.inner > 0) {
-    if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a);
-    if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a);
-    if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a);
-    return launch_fast<true, true>(stream, a);
-  }
-  const uint32_t tiles_m = (a.rows + 63) / 64, tiles_n = (a.columns + 63) / 64;
-  hipLaunchKernelGGL(gemm_f32_general_kernel, dim3(tiles_m * tiles_n, a.batches), dim3(256), 0,
-                     stream, (float*)a.out, (const float*)a.left, (const float*)a.right, a.rows,
-                     a.columns, a.inner, a.transpose_left, a.transpose_right, a.left_batch_stride,
-                     a.right_batch_stride, tiles_n);
-  return hip_status(hipGetLastError());
+  // Other shapes and alignments, and K = 0 (every load masked, zeros
+  // stored): the same kernel with element loads and stores.
+  const bool vec = aligned && chunked && a.inner > 0;
+  if (!a.transpose_left && !a.transpose_right) return launch_fast<false, false>(stream, a, vec);
+  if (!a.transpose_left && a.transpose_right) return launch_fast<false, true>(stream, a, vec);
+  if (a.transpose_left && !a.transpose_right) return launch_fast<true, false>(stream, a, vec);
+  return launch_fast<true, true>(stream, a, vec);
 }
 
 }  // namespace ipus

@@ -371,7 +371,11 @@ def test_gemm_f16_8192_sampled_rows(ipus, oracle, ctx):
                                          (132, 260, 36, False, False), (132, 260, 36, True, False),
                                          (132, 260, 36, False, True), (300, 4, 1100, True, True),
                                          (4, 516, 20, False, False), (729, 1152, 36, False, False),
-                                         (729, 132, 36, False, True)])
+                                         (729, 132, 36, False, True),
+                                         # element loads and stores (odd pitches)
+                                         (131, 257, 67, False, False), (131, 257, 67, True, True),
+                                         (257, 131, 67, True, False), (70, 66, 131, False, True),
+                                         (1, 1, 1, False, False), (300, 301, 299, False, False)])
 def test_gemm_f32(ipus, oracle, ctx, M, N, K, tl, tr):
     a = ipus.synth_f32(M * K, 31, 1, 1)
     b = ipus.synth_f32(K * N, 31, 2, 1)
@@ -381,6 +385,26 @@ def test_gemm_f32(ipus, oracle, ctx, M, N, K, tl, tr):
     B = b.reshape((N, K) if tr else (K, N)).astype(np.float64)
     want = (A.T if tl else A) @ (B.T if tr else B)
     assert max_rel(got.reshape(M, N), want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("shift", [4, 8])
+def test_gemm_f32_misaligned_pointers(ipus, ctx, shift):
+    """Left operand and output 4 or 8 bytes into their allocations: the
+    element-load mode of the same kernel."""
+    M, N, K = 256, 260, 132
+    a = ipus.synth_f32(M * K, 33, 1, 1)
+    b = ipus.synth_f32(K * N, 33, 2, 1)
+    da = ctx.upload(np.concatenate([np.zeros(shift // 4, np.float32), a]))
+    db = ctx.upload(b)
+    out = ctx.upload(np.full(M * N + 8, np.nan, np.float32))
+    ctx.launch("ipu_stack_gemm_f32", out.ptr + shift, [da.ptr + shift, db], [1, M, N, K, 0, 0, 0, 0])
+    raw = out.download(np.float32)
+    got = raw[shift // 4: shift // 4 + M * N].reshape(M, N)
+    assert np.isnan(raw[:shift // 4]).all() and np.isnan(raw[shift // 4 + M * N:]).all()
+    want = a.reshape(M, K).astype(np.float64) @ b.reshape(K, N).astype(np.float64)
+    assert max_rel(got, want) <= FP32_TOL
+    for x in (da, db, out):
+        x.free()
 
 
 def test_gemm_f32_4096_sampled_rows(ipus, ctx):
