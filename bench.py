@@ -271,20 +271,27 @@ def bench_mlp_graph(ipus, ctx, steps, warmup, settle=0):
 
 
 def mfma_calibration(ipus, ctx, blocks=1024, iterations=4096):
-    """Sustained v_mfma_f32_32x32x16_f16 rate and shader clock with register-
-    resident operands: once with fragments drawn like the headline's inputs
-    (U[-1, 1] fp16) and once with all-zero fragments.  The clock under dense
-    MFMA falls with operand entropy (power limit), so the first figure is the
-    ceiling the headline GEMM can reach on this board."""
+    """Sustained MFMA rate and shader clock with register-resident operands
+    (no memory traffic), after settle launches (~60 ms of load, as the
+    headline gets): v_mfma_f32_32x32x16_f16 on fragments drawn like the
+    headline's inputs (U[-1, 1] fp16) and on all-zero fragments, and
+    v_mfma_f32_16x16x32_f16 -- the form the GEMM and attention kernels
+    issue -- on U[-1, 1] fragments that change from one MFMA to the next.
+    The clock under dense MFMA falls with operand entropy (power limit), and
+    the 16 x 16 x 32 form draws less power per flop, so the last figure is
+    the tightest ceiling for the headline GEMM on this board."""
     out = {}
-    for name, frags in (("uniform", ipus.synth_f16(4096 * 8, 2024, 3, ipus.UNIFORM)),
-                        ("zeros", np.zeros(4096 * 8, dtype=np.float16))):
+    uniform = ipus.synth_f16(4096 * 8, 2024, 3, ipus.UNIFORM)
+    forms = (("uniform", "ipus_calibrate_mfma_f16", 32 * 32 * 16, uniform, 25),
+             ("zeros", "ipus_calibrate_mfma_f16", 32 * 32 * 16, np.zeros(4096 * 8, dtype=np.float16), 25),
+             ("uniform_16x16x32", "ipus_calibrate_mfma_f16_16x16x32", 16 * 16 * 32, uniform, 50))
+    for name, symbol, macs, frags, settle in forms:
         ops = ctx.upload(frags)
         res = ctx.alloc(16 + blocks * 256 * 4)
         sc = [4096, iterations, blocks]
-        t = timed(ctx, lambda i: ctx.launch("ipus_calibrate_mfma_f16", res, [ops], sc), 3, 1)
+        t = timed(ctx, lambda i: ctx.launch(symbol, res, [ops], sc), 5, 1, repeats=1, settle=settle)
         clocks = res.download(np.uint64)[:2]
-        flops = blocks * 4 * 8 * iterations * 32 * 32 * 16 * 2.0
+        flops = blocks * 4 * 8 * iterations * macs * 2.0
         mhz = clocks[0] / (clocks[1] / 100.0) if clocks[1] else 0.0
         out[name] = {"tflops": round(flops / (t.median * 1e-3) / 1e12, 1),
                      "clock_mhz": round(mhz)}
@@ -680,6 +687,8 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
         cal = mfma_calibration(ipus, ctx)
         if headline_tflops:
             cal["headline_frac_of_uniform"] = round(headline_tflops / cal["uniform"]["tflops"], 4)
+            cal["headline_frac_of_uniform_16x16x32"] = round(
+                headline_tflops / cal["uniform_16x16x32"]["tflops"], 4)
         results["mfma_calibration"] = cal
         log(f"mfma calibration: {cal}")
     if want("gemm_f16_layouts"):

@@ -251,6 +251,9 @@ int ipus_event_elapsed_ms(ipus_event *start, ipus_event *end, float *millisecond
  *        100 MHz ticks, then blocks*256 floats; input: operand_count
  *        fragments of 8 fp16; operand_count, iterations, blocks.  Each
  *        wave issues 8*iterations v_mfma_f32_32x32x16_f16 on its fragments.
+ *   ipus_calibrate_mfma_f16_16x16x32   the same with v_mfma_f32_16x16x32_f16
+ *        (the form the GEMM and attention kernels issue), eight fragment
+ *        pairs per lane so that consecutive MFMAs see different operands.
  *   ipus_calibrate_copy                out; input; byte_count (a multiple of
  *        16, both pointers 16-byte aligned): a plain copy with ordinary
  *        16-byte loads and stores, whose HBM traffic counters scale those of

@@ -126,7 +126,8 @@ uint64_t calibrate_output_bytes(uint32_t blocks);
 // both pointers 16-byte aligned): the HBM traffic counters' calibration.
 int launch_calibrate_copy(hipStream_t stream, void* dst, const void* src, uint32_t bytes);
 int launch_calibrate_mfma_f16(hipStream_t stream, void* out, const void* operands,
-                              uint32_t operand_count, uint32_t iterations, uint32_t blocks);
+                              uint32_t operand_count, uint32_t iterations, uint32_t blocks,
+                              bool form16 = false);
 // Stored order (AmpLeft, AmpTransposedRight, BlockMajor) -> row-major.
 int launch_to_row_major_f16(hipStream_t stream, void* dst, const void* src, uint32_t source_order,
                             uint32_t row_block, uint32_t column_block, uint32_t matrices,

@@ -616,6 +616,10 @@ const std::vector<KernelEntry>& registry() {
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_calibrate_mfma_f16(c->stream, o, i[0], s[0], s[1], s[2]);
        }},
+      {"ipus_calibrate_mfma_f16_16x16x32", 1, {"operand_count", "iterations", "blocks"},
+       [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
+         return launch_calibrate_mfma_f16(c->stream, o, i[0], s[0], s[1], s[2], true);
+       }},
       {"ipus_calibrate_copy", 1, {"byte_count"},
        [](ipus_context* c, void* o, const void* const* i, const uint32_t* s) {
          return launch_calibrate_copy(c->stream, o, i[0], s[0]);
