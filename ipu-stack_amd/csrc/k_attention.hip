@@ -764,7 +764,8 @@ int launch(hipStream_t stream, const AttentionArgs& a, float scale_log2, bool ve
 }
 }  // namespace wide
 
-// General attention: one 64-lane block per (stream, query row); any widths.
+// One 64-lane block per (stream, query row): the fallback for query/key
+// widths above 256 (any query/key width, value width up to 512).
 // Online softmax over keys one at a time (dot products by wave reduction).
 constexpr uint32_t kGeneralMaxValuePerLane = 8;  // value width <= 512
 
@@ -860,7 +861,8 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
   const bool fits = ((uint64_t)a.key_rows + kKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
   // Widths that are multiples of 8 up to 128 run in 64- or 128-wide tiles
-  // (zero padding); others take the general kernel.
+  // (zero padding); other widths take the MFMA kernel below, or the
+  // one-row-per-block kernel past its limits.
   if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 128) {
     return a.width > 64 ? dispatch_fast<128>(stream, a, scale_log2)
                         : dispatch_fast<64>(stream, a, scale_log2);
