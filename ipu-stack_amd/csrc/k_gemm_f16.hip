@@ -651,6 +651,7 @@ int launch_small(hipStream_t stream, const GemmArgs& a) {
   const uint32_t tile = tiles64 * a.batches < 64 ? 32 : 64;
   const uint32_t tiles_m = (a.rows + tile - 1) / tile;
   const uint32_t tiles_n = (a.columns + tile - 1) / tile;
+  if ((uint64_t)tiles_m * tiles_n > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
   const dim3 grid(tiles_m * tiles_n, a.batches);
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, (uint16_t*)a.out,
