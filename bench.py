@@ -671,7 +671,45 @@ ATTENTION_SETTLE_LAUNCHES = 200
 
 LEGS = ("mfma_calibration", "gemm_f16_layouts", "gemm_f32_4096", "attention_causal_s4096",
         "attention_noncausal_s2048", "memory_chain", "amp_layouts", "gelu_4096x16384",
-        "mlp_graph", "gemm_f16_256")
+        "mlp_graph", "off_fast_path", "gemm_f16_256")
+
+
+def bench_off_fast_path(ipus, ctx, steps):
+    """Shapes the fast kernels do not take (no BASELINE config uses them):
+    fp16 / fp32 GEMMs whose pitches are not multiples of 8 / 4, and attention
+    with query width 256 or value width 64 against query width 128."""
+    out = {}
+
+    def gemm(name, m, n, k, f32):
+        synth = ipus.synth_f32 if f32 else ipus.synth_f16
+        a = ctx.upload(synth(m * k, 7, 1, ipus.UNIFORM))
+        b = ctx.upload(synth(k * n, 7, 2, ipus.UNIFORM))
+        c = ctx.alloc(m * n * (4 if f32 else 2))
+        sym = "ipu_stack_gemm_f32" if f32 else "ipu_stack_gemm_f16"
+        t = timed(ctx, lambda i: ctx.launch(sym, c, [a, b], [1, m, n, k, 0, 0, 0, 0]), steps, 2,
+                  repeats=3, settle=10)
+        out[name] = leg_entry(t, 2.0 * m * n * k, "tflops",
+                              PEAK_FP32_TFLOPS if f32 else PEAK_FP16_TFLOPS)
+        for x in (a, b, c):
+            x.free()
+
+    def attention(name, streams, s, d, dv):
+        q = ctx.upload(ipus.synth_f16(streams * s * d, 5, 1, ipus.NORMAL))
+        k = ctx.upload(ipus.synth_f16(streams * s * d, 5, 2, ipus.NORMAL))
+        v = ctx.upload(ipus.synth_f16(streams * s * dv, 5, 3, ipus.NORMAL))
+        o = ctx.alloc(streams * s * dv * 4)
+        sc = [streams, s, s, d, dv, 0, 0, 0]
+        t = timed(ctx, lambda i: ctx.launch("ipu_stack_flash_attention_online_f16", o, [q, k, v], sc),
+                  steps, 2, repeats=3, settle=10)
+        out[name] = leg_entry(t, 2.0 * streams * s * s * (d + dv), "tflops", PEAK_FP16_TFLOPS)
+        for x in (q, k, v, o):
+            x.free()
+
+    gemm("gemm_f16_4096x4096x4100", 4096, 4096, 4100, False)
+    gemm("gemm_f32_4096x4096x4097", 4096, 4096, 4097, True)
+    attention("attention_16x2048_d256", 16, 2048, 256, 256)
+    attention("attention_16x2048_d128_dv64", 16, 2048, 128, 64)
+    return out
 
 
 def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
@@ -712,6 +750,9 @@ def secondary_legs(ipus, ctx, args, headline_tflops=None, only=None):
         fl = 4.0 * 128 * 128 * (s * (s + 1) / 2 if causal else s * s)
         results[key] = leg_entry(t, fl, "tflops", PEAK_FP16_TFLOPS)
         log(f"{key}: {results[key]}")
+    if want("off_fast_path"):
+        results["off_fast_path"] = bench_off_fast_path(ipus, ctx, 5)
+        log(f"off the fast paths: {results['off_fast_path']}")
     if want("memory_chain"):
         chain = bench_memory_chain(ipus, ctx, args.steps, 3)
         bytes_rw = {"copy": 2 * n * n * 2, "transpose": 2 * n * n * 2, "block_major": 2 * n * n * 2,
