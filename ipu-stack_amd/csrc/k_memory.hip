@@ -826,13 +826,19 @@ template <bool ToRowMajor>
 bool launch_amp_tile(hipStream_t stream, void* dst, const void* src, uint32_t order,
                      uint32_t matrices, uint32_t rows, uint32_t columns) {
   if (order == kOrderAmpLeft) {
+    // Row-major -> AMP-Left: 96 x 64 tiles at five workgroups per CU
+    // (8192^2: 5.34-5.37 -> 5.60-5.62 TB/s against 64 x 64 tiles at the
+    // default occupancy; 128 x 64 at four or five per CU 5.51-5.57, 96 x 64
+    // at four or six 5.42-5.55).  The reverse keeps 64 x 64.
+    constexpr uint32_t kRows = ToRowMajor ? 64 : 96;
     const uint32_t tiles_c = ceil_div(columns, 64);
     const uint64_t flat = (uint64_t)matrices * rows;
-    const uint64_t tiles = ceil_div(flat, 64) * (uint64_t)tiles_c;
+    const uint64_t tiles = ceil_div(flat, kRows) * (uint64_t)tiles_c;
     if (flat > 0xffffffffull || tiles > 0x7fffffffull) return false;
-    hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpLeft, ToRowMajor, 64, 64>),
-                       dim3((uint32_t)tiles), dim3(kThreads), 0, stream, (uint16_t*)dst,
-                       (const uint16_t*)src, (uint32_t)flat, columns, tiles_c);
+    hipLaunchKernelGGL((amp_tile_f16_kernel<kOrderAmpLeft, ToRowMajor, kRows, 64>),
+                       dim3((uint32_t)tiles), dim3(kThreads), ToRowMajor ? 0 : occupancy_lds(5, 0),
+                       stream, (uint16_t*)dst, (const uint16_t*)src, (uint32_t)flat, columns,
+                       tiles_c);
     return true;
   }
   const uint32_t tiles_c = ceil_div(columns, 64);
@@ -913,16 +919,21 @@ int launch_unpack_f16(hipStream_t stream, void* dst, const void* src, uint32_t s
   if (unpadded && source_order == kUnpackAmpOutput && out_tiles <= 0x7fffffffull &&
       matrices <= 65535) {
     const uint32_t tiles_c = ceil_div(physical_columns, 64);
+    // Six workgroups per CU (8192^2: 5.36-5.39 -> 5.53-5.56 TB/s; five
+    // 5.46-5.49, seven 5.45-5.47, four with 64-row tiles 5.47).
     hipLaunchKernelGGL(unpack_amp_output_f16_kernel, dim3((uint32_t)out_tiles, matrices),
-                       dim3(kThreads), 0, stream, (uint16_t*)dst, (const uint16_t*)src,
+                       dim3(kThreads), occupancy_lds(6, 0), stream, (uint16_t*)dst, (const uint16_t*)src,
                        physical_rows, physical_columns, tiles_c);
   } else if (unpadded && source_order == kUnpackAmpTransposedLeft && physical_columns % 8 == 0 &&
              matrices <= 65535 &&
              (uint64_t)(physical_rows / kMicro) * ceil_div(physical_columns, 8 * (kThreads / 2)) <=
                  0x7fffffffull) {
     const uint32_t col_groups = ceil_div(physical_columns, 8 * (kThreads / 2));
+    // Two workgroups per CU (8192^2: 5.71-5.72 -> 5.78-5.80 TB/s; one
+    // 5.55-5.58, three 5.75-5.77).
     hipLaunchKernelGGL(unpack_amp_transposed_left_f16_kernel,
-                       dim3(physical_rows / kMicro * col_groups, matrices), dim3(kThreads), 0,
+                       dim3(physical_rows / kMicro * col_groups, matrices), dim3(kThreads),
+                       occupancy_lds(2, 0),
                        stream, (uint16_t*)dst, (const uint16_t*)src, physical_rows,
                        physical_columns, col_groups);
   } else {
