@@ -1247,12 +1247,12 @@ extern "C" int ipus_build_package(const ipus_graph* g, const ipus_package_config
     ts.external = true;
     ts.constant.resize(table.size() * 4);
     memcpy(ts.constant.data(), table.data(), ts.constant.size());
-    const int out = b.new_slot(shape, precision);
-    b.emit("ipu_stack_unshard", out, {{slot, 0}, {tslot, 0}},
+    const int unsharded = b.new_slot(shape, precision);
+    b.emit("ipu_stack_unshard", unsharded, {{slot, 0}, {tslot, 0}},
            {shard_count, (uint32_t)shape.size(), (uint32_t)f->format.order, f->format.row_block,
             f->format.column_block, (uint32_t)esize,
             (uint32_t)std::min<uint64_t>(max_elements, 0xffffffffull)});
-    b.env[in.value] = out;
+    b.env[in.value] = unsharded;
   }
   if (int e = b.lower_ops(g->root.operations)) return e;
   for (size_t i = 0; i < g->outputs.size(); ++i) {
