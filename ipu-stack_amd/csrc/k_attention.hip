@@ -572,7 +572,7 @@ constexpr uint32_t kKeys = 32;
 constexpr uint32_t kQueries = 64;  // per workgroup
 
 template <uint32_t DMAX, uint32_t DVMAX, bool Vec8>
-__global__ __launch_bounds__(kThreads) void attention_wide_kernel(
+__global__ __launch_bounds__(kThreads, DVMAX > 256 ? 1 : 2) void attention_wide_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t query_rows, uint32_t key_rows, uint32_t width,
     uint32_t value_width, float scale_log2, bool causal, bool out_f16, uint32_t q_heads,
@@ -685,10 +685,11 @@ __global__ __launch_bounds__(kThreads) void attention_wide_kernel(
       s[kt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (uint32_t ks = 0; ks < kKS; ++ks) {
-        if (ks >= nks) break;
-        const half8_t kf = __builtin_bit_cast(
-            half8_t, *reinterpret_cast<const u32x4*>(lk + (kbase ^ (ks << 6)) + 16 * kt * kKRow));
-        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s[kt], 0, 0, 0);
+        if (ks < nks) {
+          const half8_t kf = __builtin_bit_cast(
+              half8_t, *reinterpret_cast<const u32x4*>(lk + (kbase ^ (ks << 6)) + 16 * kt * kKRow));
+          s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s[kt], 0, 0, 0);
+        }
       }
     }
     // Online softmax in log2 units; masked keys are -inf.  A query whose
@@ -721,12 +722,13 @@ __global__ __launch_bounds__(kThreads) void attention_wide_kernel(
     // Output: o[dt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi].
 #pragma unroll
     for (uint32_t dt = 0; dt < kDT; ++dt) {
-      if (dt >= ndt) break;
-      const uint8_t* p = lv + (vbase ^ (dt << 5));
-      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
-      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kVRow));
-      const half8_t vf = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pp, o[dt] * alpha, 0, 0, 0);
+      if (dt < ndt) {
+        const uint8_t* p = lv + (vbase ^ (dt << 5));
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kVRow));
+        const half8_t vf = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pp, o[dt] * alpha, 0, 0, 0);
+      }
     }
   }
   const float inv = 1.0f / sum_of_query(l_run);
