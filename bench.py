@@ -675,9 +675,11 @@ LEGS = ("mfma_calibration", "gemm_f16_layouts", "gemm_f32_4096", "attention_caus
 
 
 def bench_off_fast_path(ipus, ctx, steps):
-    """Shapes the fast kernels do not take (no BASELINE config uses them):
-    fp16 / fp32 GEMMs whose pitches are not multiples of 8 / 4, and attention
-    with query width 256 or value width 64 against query width 128."""
+    """Shapes no BASELINE config uses, on the kernels' other paths: fp16 /
+    fp32 GEMMs whose pitches are not multiples of 8 / 4 (element-gathering
+    tile kernels), attention at width 256 (the fast kernel's 256-wide tiles)
+    and at value width 64 beside query width 128 (the MFMA kernel for uneven
+    widths)."""
     out = {}
 
     def gemm(name, m, n, k, f32):

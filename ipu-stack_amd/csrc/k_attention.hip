@@ -7,16 +7,17 @@
 // crates/ipu-tests/src/diagnostic.rs:711-780 (key j allowed iff j <= i when
 // causal, 741-745; scale default 1/sqrt(width), 733-736).
 //
-// Fast kernel (width == value width, a multiple of 8 up to 128, computed in
-// tiles 64 or 128 columns wide with zero padding):
-//   * 256 threads = 4 waves; a wave owns 32 queries (two tiles of 16), a
-//     workgroup 128 queries of one stream; two workgroups share a CU (launch
-//     bound), so one SIMD runs the softmax of one wave while the MFMA pipe
-//     serves the other;
-//   * keys stream through LDS in blocks of 64 with two stages.  K and V tiles
+// Fast kernel (width == value width, a multiple of 8 up to 256, computed in
+// tiles 64, 128 or 256 columns wide with zero padding):
+//   * 256 threads = 4 waves; a wave owns 32 queries (two tiles of 16; one
+//     tile at 256 columns), a workgroup 128 (64) queries of one stream; two
+//     workgroups share a CU (launch bound), so one SIMD runs the softmax of
+//     one wave while the MFMA pipe serves the other;
+//   * keys stream through LDS in blocks of 64 (32 at 256 columns) with two
+//     stages.  K and V tiles
 //     are copied global -> LDS with buffer_load ... lds (16 bytes per lane, no
 //     staging registers; rows past the end of the stream read as 0), both
-//     stored row-major [64 keys][D] with an XOR swizzle of 16-byte chunks;
+//     stored row-major [keys][D] with an XOR swizzle of 16-byte chunks;
 //   * v_mfma_f32_16x16x32_f16 throughout: under the board's power limit it
 //     sustains a higher clock than 32 x 32 x 16 on changing operands;
 //   * software pipeline: step j runs ONE MFMA cluster holding the scores of
@@ -33,7 +34,7 @@
 //     registers, and the matching V^T fragments come from the row-major V
 //     tile through ds_read_b64_tr_b16, whose 4-key runs are chosen to follow
 //     the score accumulator's key order;
-//   * each fragment read feeds two MFMAs (the wave's two query tiles);
+//   * each fragment read feeds one MFMA per query tile of the wave;
 //   * the reference point (running max) moves only when some probability of
 //     a block would exceed 2^kRescaleSlack, which the block's probability
 //     sum bounds, so no max over the scores is taken on the common path:
@@ -59,9 +60,21 @@ namespace ipus {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kQueriesPerWave = 32;
-constexpr int kQueriesPerBlock = 128;
-constexpr int kKeysPerBlock = 64;
+// Fast-kernel shape for tile width D: 16-query tiles per wave and keys per
+// block.  Up to 128 columns a wave owns two query tiles (32 queries) and a
+// block is 64 keys; at 256 columns one tile and 32 keys keep the registers
+// (output accumulators, Q fragments) within two waves per SIMD and the two
+// LDS stages within two workgroups per CU.
+template <int D>
+struct Fast {
+  static constexpr int kQT = D > 128 ? 1 : 2;           // 16-query tiles per wave
+  static constexpr int kKeys = D > 128 ? 32 : 64;       // keys per block
+  static constexpr int kQueriesPerWave = 16 * kQT;
+  static constexpr int kQueriesPerBlock = 4 * kQueriesPerWave;  // per workgroup
+  static constexpr int kKT = kKeys / 16;                // 16-key score tiles per block
+  static constexpr int kHalves = kKeys / 32;            // 32-key output contractions per block
+};
+constexpr int kMaxKeysPerBlock = 64;
 constexpr uint32_t kBlocksPerGroup = 2;  // query blocks per workgroup, run back to back
 constexpr float kLog2e = 1.4426950408889634f;
 // A block whose probabilities, taken against the current reference point,
@@ -73,27 +86,29 @@ typedef short short4_t __attribute__((vector_size(8)));
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
-// Tiles of 64 keys x D fp16, rows of D * 2 bytes, 16-byte chunks swizzled by
-// row.  K is read with ds_read_b128 (each 16-lane group: 16 consecutive rows
-// of one chunk), V with ds_read_b64_tr_b16 (each 16-lane group: 4 consecutive
-// rows x 32 bytes, 16 consecutive rows per instruction).  The XORs below read
-// both without bank conflicts (SQ_LDS_BANK_CONFLICT = 0 in a probe of the two
-// patterns; they depend only on the row's low bits, which a DMA step of
-// kThreads / kChunks rows leaves alone).
+// Tiles of Fast<D>::kKeys keys x D fp16, rows of D * 2 bytes, 16-byte
+// chunks swizzled by row.  K is read with ds_read_b128 (each 16-lane group:
+// 16 consecutive rows of one chunk), V with ds_read_b64_tr_b16 (each 16-lane
+// group: 4 consecutive rows x 32 bytes, 16 consecutive rows per
+// instruction).  The XORs below read both without bank conflicts
+// (SQ_LDS_BANK_CONFLICT = 0 in a probe of the two patterns on 128- and
+// 256-byte rows).  They depend only on the row's low bits and change only
+// the low 4 bits of the chunk index, and a bank is fixed by the byte offset
+// modulo 256, so 512-byte rows (D = 256) see the 256-byte rows' pattern.
 template <int D>
 struct KvTile {
   static constexpr uint32_t kRowBytes = D * 2;
   static constexpr uint32_t kChunks = D / 8;
-  static constexpr uint32_t kBytes = kKeysPerBlock * D * 2;
+  static constexpr uint32_t kBytes = Fast<D>::kKeys * D * 2;
   static constexpr uint32_t kDma = kBytes / 16 / kThreads;  // DMA instructions per thread
 };
 template <int D>
 __device__ __forceinline__ uint32_t k_swz(uint32_t row) {
-  return D == 128 ? (row & 15u) : (row & 7u);
+  return D >= 128 ? (row & 15u) : (row & 7u);
 }
 template <int D>
 __device__ __forceinline__ uint32_t v_swz(uint32_t row) {
-  return D == 128 ? ((row & 7u) << 1) : (row & 7u);
+  return D >= 128 ? ((row & 7u) << 1) : (row & 7u);
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -115,9 +130,11 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds,
 // Byte offset within a key block of the chunk this thread's first DMA
 // instruction fetches: instruction i of thread t fills LDS slot i * 256 + t,
 // so it loads the chunk that the swizzle places there.  Instruction i covers
-// the rows kThreads / kChunks * i further on with the same swizzled chunk (the
-// swizzles depend only on row bits that this step leaves alone), so the other
-// instructions add a wave-uniform row offset.  row_bytes is the global row
+// the rows kThreads / kChunks * i further on; the other instructions add a
+// wave-uniform row offset.  The swizzles depend on row bits 0-3 (K at D >=
+// 128) or 0-2, which a step of 16 or 32 rows leaves alone; at D = 256 a step
+// is 8 rows, so the odd instructions' K chunks are those of row + 8
+// (first_row = 8), the even ones' those of row.  row_bytes is the global row
 // pitch: width * 2 for a contiguous [streams, rows, width] tensor, heads *
 // width * 2 for a head of an unsplit [batch, rows, heads * width].  Chunks at
 // or past the width (a width below the tile's D, padded) get an offset past
@@ -125,40 +142,43 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds,
 // offset (< 2^31) stays above the range (< 0x7fff0000) without wrapping.
 constexpr uint32_t kPadOffset = 0x80000000u;
 template <int D, bool IsK>
-__device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes, uint32_t width) {
+__device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes, uint32_t width,
+                                              uint32_t first_row = 0) {
   const uint32_t row = threadIdx.x / KvTile<D>::kChunks, phys = threadIdx.x % KvTile<D>::kChunks;
-  const uint32_t chunk = phys ^ (IsK ? k_swz<D>(row) : v_swz<D>(row));
+  const uint32_t srow = row + first_row;
+  const uint32_t chunk = phys ^ (IsK ? k_swz<D>(srow) : v_swz<D>(srow));
   return chunk * 8 < width ? row * row_bytes + chunk * 16 : kPadOffset;
 }
 
 // Key blocks of query block qb: causal blocks stop at the block's last query.
-template <bool Causal>
+template <int D, bool Causal>
 __device__ __forceinline__ uint32_t key_blocks(uint32_t qb, uint32_t query_rows, uint32_t key_rows) {
+  constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock, kKeys = Fast<D>::kKeys;
   uint32_t key_end = key_rows;
   if (Causal) {
-    const uint32_t q0 = qb * kQueriesPerBlock;
-    const uint32_t last_q = q0 + kQueriesPerBlock < query_rows ? q0 + kQueriesPerBlock : query_rows;
+    const uint32_t q0 = qb * kQPB;
+    const uint32_t last_q = q0 + kQPB < query_rows ? q0 + kQPB : query_rows;
     key_end = last_q < key_rows ? last_q : key_rows;
   }
-  return (key_end + kKeysPerBlock - 1) / kKeysPerBlock;
+  return (key_end + kKeys - 1) / kKeys;
 }
 
 // The wave's Q fragments for query block qb (second MFMA operand of the
 // scores): tile qt, k step ks holds Q[query][32 ks + 8 (l / 16) .. +7] of
-// query qb * 128 + 32 wave + 16 qt + l % 16 (clamped to the last row;
-// padding columns are 0).
+// query qb * kQueriesPerBlock + wave * kQueriesPerWave + 16 qt + l % 16
+// (clamped to the last row; padding columns are 0).
 template <int D>
-__device__ __forceinline__ void load_q(half8_t (&qf)[2][D / 32], const uint16_t* __restrict__ query,
+__device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][D / 32], const uint16_t* __restrict__ query,
                                        uint32_t stream, uint32_t qb, uint32_t query_rows,
                                        uint32_t width, uint32_t q_heads) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t r16 = lane % 16, g4 = lane / 16;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const uint32_t wq0 = qb * kQueriesPerBlock + wave_s * kQueriesPerWave;
+  const uint32_t wq0 = qb * Fast<D>::kQueriesPerBlock + wave_s * Fast<D>::kQueriesPerWave;
   const uint32_t q_pitch = q_heads * width;
   const uint16_t* Q = query + (uint64_t)(stream / q_heads) * query_rows * q_pitch + (stream % q_heads) * width;
 #pragma unroll
-  for (uint32_t qt = 0; qt < 2; ++qt) {
+  for (uint32_t qt = 0; qt < Fast<D>::kQT; ++qt) {
     uint32_t q = wq0 + 16 * qt + r16;
     q = q < query_rows ? q : query_rows - 1;
 #pragma unroll
@@ -175,14 +195,17 @@ __device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
     uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
-    uint32_t v_heads, half8_t (&qf)[2][D / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
+    uint32_t v_heads, half8_t (&qf)[Fast<D>::kQT][D / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
+  constexpr int kQT = Fast<D>::kQT, kKT = Fast<D>::kKT, kHalves = Fast<D>::kHalves;
+  constexpr uint32_t kKeys = Fast<D>::kKeys;
+  constexpr uint32_t kQPW = Fast<D>::kQueriesPerWave, kQPB = Fast<D>::kQueriesPerBlock;
   constexpr uint32_t kKS = D / 32;  // k steps (32 columns) of the score MFMAs
   constexpr uint32_t kDT = D / 16;  // output d tiles (16 columns)
-  constexpr uint32_t kPairs = 4 * kKS;  // score MFMA pairs (query tiles 0, 1) per key block
+  constexpr uint32_t kPairs = kKT * kKS;  // score MFMA groups (every query tile) per key block
   constexpr uint32_t kRB = KvTile<D>::kRowBytes;
   constexpr uint32_t kTile = KvTile<D>::kBytes;
   constexpr uint32_t kDmaRows = kThreads / KvTile<D>::kChunks;  // rows per DMA instruction
-  static_assert(kPairs == 2 * kDT, "one output MFMA pair per score MFMA pair");
+  static_assert(kPairs == kHalves * kDT, "one output MFMA group per score MFMA group");
   // Two stages, each a distinct LDS object so the compiler can see that the
   // DMA into one stage never aliases the fragment reads of the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTile];
@@ -190,11 +213,11 @@ __device__ __forceinline__ void attention_block(
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTile];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTile];
 
-  const uint32_t q0 = qb * kQueriesPerBlock;
+  const uint32_t q0 = qb * kQPB;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t r16 = lane % 16, g4 = lane / 16;
   const uint32_t wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
-  const uint32_t wq0 = q0 + wave_s * kQueriesPerWave;  // first query of this wave
+  const uint32_t wq0 = q0 + wave_s * kQPW;  // first query of this wave
 
   // Stream s of an operand with h heads is head s % h of matrix s / h of a
   // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
@@ -206,35 +229,44 @@ __device__ __forceinline__ void attention_block(
       (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + width * 2u), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + width * 2u), kBufferFlags);
+  // K chunks of even and odd DMA instructions (they differ only at D = 256).
   const uint32_t k_voff = kv_offset<D, true>(k_row_bytes, width);
+  const uint32_t k_voff_odd = kDmaRows % 16 == 0 ? k_voff : kv_offset<D, true>(k_row_bytes, width, kDmaRows);
   const uint32_t v_voff = kv_offset<D, false>(v_row_bytes, width);
+  static_assert(kDmaRows % 8 == 0, "the V swizzle depends on row bits 0-2 only");
 
-  const uint32_t nblocks = key_blocks<Causal>(qb, query_rows, key_rows);
-  const uint32_t k_block_bytes = kKeysPerBlock * k_row_bytes;
-  const uint32_t v_block_bytes = kKeysPerBlock * v_row_bytes;
+  const uint32_t nblocks = key_blocks<D, Causal>(qb, query_rows, key_rows);
+  const uint32_t k_block_bytes = kKeys * k_row_bytes;
+  const uint32_t v_block_bytes = kKeys * v_row_bytes;
   // Blocks this wave computes scores for (causal: keys <= its last query).
   // Every such block holds at least one allowed key per query of the wave.
   uint32_t nproc = nblocks;
   if (Causal) {
-    const uint32_t lim = (wq0 + kQueriesPerWave - 1) / kKeysPerBlock + 1;
+    const uint32_t lim = (wq0 + kQPW - 1) / kKeys + 1;
     nproc = lim < nproc ? lim : nproc;
   }
 
-  float4_t o[kDT][2];
+  float4_t o[kDT][kQT];
 #pragma unroll
   for (uint32_t dt = 0; dt < kDT; ++dt)
 #pragma unroll
-    for (uint32_t qt = 0; qt < 2; ++qt) o[dt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run[2] = {-INFINITY, -INFINITY};  // reference points, log2 units (scaled)
-  float l_run[2] = {0.0f, 0.0f};            // this lane's share of the row sums
-  half8_t pp[2][2];  // fp16 probabilities of the last softmax [key half kk][qt]
+    for (uint32_t qt = 0; qt < kQT; ++qt) o[dt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run[kQT];  // reference points, log2 units (scaled)
+  float l_run[kQT];  // this lane's share of the row sums
+  uint32_t qi[kQT];  // this lane's query in tile qt
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
+  for (int qt = 0; qt < kQT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.0f;
+    qi[qt] = wq0 + 16 * qt + r16;
+  }
+  half8_t pp[kHalves][kQT];  // fp16 probabilities of the last softmax [key half kk][qt]
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+  for (int kk = 0; kk < kHalves; ++kk)
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
       for (int e = 0; e < 8; ++e) pp[kk][qt][e] = (half_t)0.0f;  // "block -1"
-  uint32_t qi[2] = {wq0 + r16, wq0 + 16 + r16};
 
   // Score accumulator s[kt][qt] (v_mfma_f32_16x16x32_f16 of K tile kt as the
   // first operand): element e is key 16 kt + 4 (l / 16) + e of query qt.
@@ -278,7 +310,7 @@ __device__ __forceinline__ void attention_block(
   auto dma_k = [&](uint32_t i, uint8_t* nk, uint32_t bytes) __attribute__((always_inline)) {
     uint32_t so = bytes + i * kDmaRows * k_row_bytes;
     asm volatile("" : "+s"(so));
-    dma16(k_rsrc, nk + (i * kThreads + wave_s * kWave) * 16, k_voff + so);
+    dma16(k_rsrc, nk + (i * kThreads + wave_s * kWave) * 16, (i % 2 ? k_voff_odd : k_voff) + so);
   };
   auto dma_v = [&](uint32_t i, uint8_t* nv, uint32_t bytes) __attribute__((always_inline)) {
     uint32_t so = bytes + i * kDmaRows * v_row_bytes;
@@ -293,19 +325,19 @@ __device__ __forceinline__ void attention_block(
   // each into the stage last read in step j - 1.  Pair p of the cluster is
   // score pair (k step p / 4, key tile p % 4) and output pair (half p / kDT,
   // d tile p % kDT), each over query tiles 0 and 1 with one fragment read.
-  auto cluster = [&]<bool WithPv>(float4_t (*s)[2], const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
+  auto cluster = [&]<bool WithPv>(float4_t (*s)[kQT], const uint8_t* lk, const uint8_t* lv, uint8_t* nk,
                                    uint8_t* nv, uint32_t kbi) __attribute__((always_inline)) {
     const uint32_t next = kbi + 1 < nblocks ? kbi + 1 : (chain ? 0u : kbi);
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) s[kt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int qt = 0; qt < kQT; ++qt) s[kt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // Fragments two pairs ahead.
     constexpr uint32_t kAhead = 2;
     half8_t kf[kAhead], vf[kAhead];
 #pragma unroll
     for (uint32_t p = 0; p < kAhead; ++p) {
-      kf[p] = kfrag(lk, p % 4, p / 4);
+      kf[p] = kfrag(lk, p % kKT, p / kKT);
       if constexpr (WithPv) vf[p] = vfrag(lv, p % kDT, p / kDT);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -314,15 +346,15 @@ __device__ __forceinline__ void attention_block(
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (uint32_t p = 0; p < kPairs; ++p) {
-      const uint32_t ks = p / 4, kt = p % 4, kk = p / kDT, dt = p % kDT;
+      const uint32_t ks = p / kKT, kt = p % kKT, kk = p / kDT, dt = p % kDT;
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kQT; ++qt) {
         s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[p % kAhead], qf[qt][ks], s[kt][qt], 0, 0, 0);
         if constexpr (WithPv)
           o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[p % kAhead], pp[kk][qt], o[dt][qt], 0, 0, 0);
       }
       if (p + kAhead < kPairs) {
-        kf[p % kAhead] = kfrag(lk, (p + kAhead) % 4, (p + kAhead) / 4);
+        kf[p % kAhead] = kfrag(lk, (p + kAhead) % kKT, (p + kAhead) / kKT);
         if constexpr (WithPv) vf[p % kAhead] = vfrag(lv, (p + kAhead) % kDT, (p + kAhead) / kDT);
       }
       // DMA instructions spread over the pairs: K tile first, then V.
@@ -340,20 +372,20 @@ __device__ __forceinline__ void attention_block(
   // Output update of the previous block alone (V tile lv).
   auto pv_only = [&](const uint8_t* lv) __attribute__((always_inline)) {
 #pragma unroll
-    for (uint32_t kk = 0; kk < 2; ++kk)
+    for (uint32_t kk = 0; kk < kHalves; ++kk)
 #pragma unroll
       for (uint32_t dt = 0; dt < kDT; ++dt) {
         const half8_t v = vfrag(lv, dt, kk);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < kQT; ++qt)
           o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v, pp[kk][qt], o[dt][qt], 0, 0, 0);
       }
   };
   // Softmax of block kbi.  s[kt][qt][e] is the score of key kb + 16 kt +
   // 4 (l / 16) + e for query qi[qt]; the result goes to pp.
-  auto softmax = [&](float4_t (*s)[2], uint32_t kbi) __attribute__((always_inline)) {
-    const uint32_t kb = kbi * kKeysPerBlock;
-    const bool need_mask = (Causal && kb + kKeysPerBlock - 1 > wq0) || kb + kKeysPerBlock > key_rows;
+  auto softmax = [&](float4_t (*s)[kQT], uint32_t kbi) __attribute__((always_inline)) {
+    const uint32_t kb = kbi * kKeys;
+    const bool need_mask = (Causal && kb + kKeys - 1 > wq0) || kb + kKeys > key_rows;
     if (need_mask) {
       // Key kb + 4 (l / 16) + x is allowed for query qi iff x <= lim (the
       // last allowed key is min(qi, key_rows - 1) causal, key_rows - 1
@@ -361,18 +393,18 @@ __device__ __forceinline__ void attention_block(
       // VCC and one select per score; the scores come straight from MFMAs,
       // and the hazard padding the compiler gives its own VALU reads of MFMA
       // results does not cover inline assembly: 24 wait states first.
-      int lim[2];
+      int lim[kQT];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kQT; ++qt) {
         const uint32_t last = Causal && qi[qt] < key_rows - 1 ? qi[qt] : key_rows - 1;
         lim[qt] = (int)last - (int)(kb + 4 * g4);
       }
       const float ninf = -INFINITY;
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             asm volatile("v_cmp_gt_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %0, %3, vcc"
@@ -385,12 +417,12 @@ __device__ __forceinline__ void attention_block(
     // consumes, added in pairs and quads in fp16 (each p <= 2^kRescaleSlack
     // on the accepted path, so a quad sum stays far inside the fp16 range
     // and carries at most two roundings), then accumulated in fp32 by v_dot2.
-    auto exps = [&](const float* neg_m, half8_t (*pf)[2], float* sum) __attribute__((always_inline)) {
+    auto exps = [&](const float* neg_m, half8_t (*pf)[kQT], float* sum) __attribute__((always_inline)) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < kQT; ++qt) {
         sum[qt] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < kHalves; ++kk) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             pf[kk][qt][e] = (half_t)__builtin_amdgcn_exp2f(
@@ -405,21 +437,25 @@ __device__ __forceinline__ void attention_block(
     // 2^kRescaleSlack, found without a max over the scores: every p is at
     // most its lane's block sum, so sums <= 2^kRescaleSlack accept the block
     // (overflow to inf and NaN, as against the -inf start, fail the test).
-    // Otherwise each query's max over its 64 keys (the four lanes that hold
+    // Otherwise each query's max over the block's keys (the four lanes that hold
     // it, so they share one reference point; finite, as every processed block
     // holds an allowed key per query) becomes its reference point, the
     // output and sum are rescaled, and the probabilities recomputed (all
     // <= 1).  Exact for any reference point.
-    half8_t pf[2][2];
-    float sum[2];
-    float neg_m[2] = {-m_run[0], -m_run[1]};
-    exps(neg_m, pf, sum);
-    if (__any(!(sum[0] <= kSumLimit) || !(sum[1] <= kSumLimit))) {
+    half8_t pf[kHalves][kQT];
+    float sum[kQT], neg_m[kQT];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) neg_m[qt] = -m_run[qt];
+    exps(neg_m, pf, sum);
+    bool over = false;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) over = over || !(sum[qt] <= kSumLimit);
+    if (__any(over)) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
         float mx = s[0][qt][0];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kt][qt][e]);
         mx = max_of_query(mx * scale_log2);
@@ -434,11 +470,11 @@ __device__ __forceinline__ void attention_block(
       exps(neg_m, pf, sum);
     }
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) l_run[qt] += sum[qt];
+    for (int qt = 0; qt < kQT; ++qt) l_run[qt] += sum[qt];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < kHalves; ++kk)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) pp[kk][qt] = pf[kk][qt];
+      for (int qt = 0; qt < kQT; ++qt) pp[kk][qt] = pf[kk][qt];
   };
 
   auto step = [&](const uint8_t* lk, const uint8_t* lv, uint8_t* nk, uint8_t* nv, uint32_t kbi)
@@ -452,7 +488,7 @@ __device__ __forceinline__ void attention_block(
     // probabilities pp starts with, and past the wave's last block every key
     // is masked, so the softmax yields zeros and only the pending output
     // update of the wave's last block counts.
-    float4_t s[4][2];
+    float4_t s[kKT][kQT];
     cluster.template operator()<true>(s, lk, lv, nk, nv, kbi);
     softmax(s, kbi);
   };
@@ -485,7 +521,7 @@ __device__ __forceinline__ void attention_block(
 
   // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < kQT; ++qt) {
     const float inv = 1.0f / sum_of_query(l_run[qt]);
     if (qi[qt] < query_rows) {
       const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * width;
@@ -522,7 +558,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
     uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
-  const uint32_t qblocks = (query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock;
+  const uint32_t qblocks = (query_rows + kQPB - 1) / kQPB;
   const uint32_t per_stream = (qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup;
   const uint32_t total = per_stream * streams;
   uint32_t pid = blockIdx.x;
@@ -536,7 +573,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   };
   const uint32_t pos0 = i * kBlocksPerGroup;
   const uint32_t reps = qblocks - pos0 < kBlocksPerGroup ? qblocks - pos0 : kBlocksPerGroup;
-  half8_t qf[2][D / 32];
+  half8_t qf[Fast<D>::kQT][D / 32];
   load_q<D>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
   bool loaded = false;  // this block's first K tile and Q fragments were fetched by the last one
   for (uint32_t rep = 0; rep < reps; ++rep) {
@@ -545,7 +582,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     const uint32_t qb = qb_at(pos0 + rep);
     // A block with an even key block count ends in stage 1, so its last
     // step can fetch the next block's first K tile into stage 0.
-    const bool chain = rep + 1 < reps && key_blocks<Causal>(qb, query_rows, key_rows) % 2 == 0;
+    const bool chain = rep + 1 < reps && key_blocks<D, Causal>(qb, query_rows, key_rows) % 2 == 0;
     if (rep > 0 && !loaded) load_q<D>(qf, query, stream, qb, query_rows, width, q_heads);
     attention_block<D, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
                                        width, scale_log2, q_heads, k_heads, v_heads, qf, loaded,
@@ -827,7 +864,8 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
 
 template <int D, bool Causal, bool OutF16>
 int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
-  const uint32_t qblocks = (a.query_rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock;
+  const uint32_t qblocks = (a.query_rows + kQPB - 1) / kQPB;
   const uint64_t blocks = (uint64_t)((qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup) * a.streams;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
   hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
@@ -861,11 +899,12 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   // descriptor with a 31-bit byte range; the offsets of the last block's
   // rows (up to 63 past the end) and of padding chunks stay below 2^32.
   const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
-  const bool fits = ((uint64_t)a.key_rows + kKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
-  // Widths that are multiples of 8 up to 128 run in 64- or 128-wide tiles
-  // (zero padding); other widths take the MFMA kernel below, or the
-  // one-row-per-block kernel past its limits.
-  if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 128) {
+  const bool fits = ((uint64_t)a.key_rows + kMaxKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
+  // Equal widths that are multiples of 8 up to 256 run in 64-, 128- or
+  // 256-wide tiles (zero padding); other widths take the MFMA kernel below,
+  // or the one-row-per-block kernel past its limits.
+  if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 256) {
+    if (a.width > 128) return dispatch_fast<256>(stream, a, scale_log2);
     return a.width > 64 ? dispatch_fast<128>(stream, a, scale_log2)
                         : dispatch_fast<64>(stream, a, scale_log2);
   }

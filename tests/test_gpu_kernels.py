@@ -445,7 +445,9 @@ def attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal, scale=None
                                              (1, 512, 512, 64), (4, 64, 64, 128),
                                              (2, 100, 37, 128), (1, 19, 17, 72),
                                              (2, 130, 130, 96), (1, 70, 90, 40),
-                                             (2, 64, 64, 8), (1, 256, 200, 120)])
+                                             (2, 64, 64, 8), (1, 256, 200, 120),
+                                             (2, 200, 200, 256), (1, 96, 130, 248),
+                                             (3, 65, 33, 136)])
 def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, d, causal)
     assert fp16_close(got, want, FP16_TOL)
@@ -459,20 +461,23 @@ def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
                                                 (1, 129, 300, 256, 256), (1, 70, 90, 120, 264),
                                                 (1, 40, 50, 300, 40)])
 def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d, dv):
-    """Widths the fast kernel does not take (query/key width above 128, value
-    width different from it, widths not a multiple of 8) run on the MFMA
-    kernel for other widths (query/key width up to 256, value width up to
-    512), and query/key widths above 256 on the one-row-per-block kernel."""
+    """Widths the fast kernel does not take (value width different from the
+    query width, widths not a multiple of 8) run on the MFMA kernel for other
+    widths (query/key width up to 256, value width up to 512), and query/key
+    widths above 256 on the one-row-per-block kernel; equal widths that are
+    multiples of 8 up to 256 here run the fast kernel's 256-wide tiles."""
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal)
     assert fp16_close(got, want, FP16_TOL)
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal):
-    """Width 136 (the MFMA kernel for other widths) at 16 streams x 2048
-    rows, fp16 output, checked on sampled rows."""
+@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120)])
+def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal, d, dv):
+    """Widths 136 and 256 (the fast kernel's 256-wide tiles) and query width
+    136 with value width 120 (the MFMA kernel for other widths) at 16 streams
+    x 2048 rows, fp16 output, checked on sampled rows."""
     rows = [0, 1, 63, 64, 500, 1023, 1024, 2047, 2048 + 5, 16 * 2048 - 1, 7 * 2048 + 1300]
-    got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, 136, 136, causal,
+    got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, d, dv, causal,
                                out_f16=True, rows=rows)
     assert fp16_close(got, want, FP16_TOL)
 
@@ -504,7 +509,8 @@ def test_attention_reference_smoke_tolerance(ipus, oracle, ctx):
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("streams,s,d,amp", [(2, 512, 128, 8.0), (2, 384, 64, 12.0),
-                                            (1, 300, 96, 4.0)])
+                                            (1, 300, 96, 4.0), (2, 320, 256, 6.0),
+                                            (1, 200, 200, 5.0)])
 def test_attention_moving_reference_point(ipus, oracle, ctx, causal, streams, s, d, amp):
     """Scores that keep rising along the keys (large queries, keys with a
     rising offset) move the kernel's reference point in many blocks, so the
@@ -524,7 +530,7 @@ def test_attention_moving_reference_point(ipus, oracle, ctx, causal, streams, s,
     assert fp16_close(got, want, FP16_TOL)
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 def test_attention_after_nan_filled_lds(ipus, oracle, ctx, d):
     """A GEMM over all-NaN operands first leaves NaN patterns in the LDS of
     every CU; the attention that follows must not pick any of them up (its
