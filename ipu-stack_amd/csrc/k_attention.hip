@@ -167,8 +167,8 @@ __device__ __forceinline__ uint32_t key_blocks(uint32_t qb, uint32_t query_rows,
 // scores): tile qt, k step ks holds Q[query][32 ks + 8 (l / 16) .. +7] of
 // query qb * kQueriesPerBlock + wave * kQueriesPerWave + 16 qt + l % 16
 // (clamped to the last row; padding columns are 0).
-template <int D>
-__device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][D / 32], const uint16_t* __restrict__ query,
+template <int D, int DC>
+__device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][DC / 32], const uint16_t* __restrict__ query,
                                        uint32_t stream, uint32_t qb, uint32_t query_rows,
                                        uint32_t width, uint32_t q_heads) {
   const uint32_t lane = threadIdx.x % kWave;
@@ -182,7 +182,7 @@ __device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][D / 32], cons
     uint32_t q = wq0 + 16 * qt + r16;
     q = q < query_rows ? q : query_rows - 1;
 #pragma unroll
-    for (uint32_t ks = 0; ks < D / 32; ++ks) {
+    for (uint32_t ks = 0; ks < DC / 32; ++ks) {
       const uint32_t d0 = ks * 32 + g4 * 8;
       qf[qt][ks] = __builtin_bit_cast(
           half8_t, d0 < width ? load16(Q + (uint64_t)q * q_pitch + d0) : u32x4{0, 0, 0, 0});
@@ -190,17 +190,18 @@ __device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][D / 32], cons
   }
 }
 
-template <int D, bool Causal, bool OutF16>
+template <int D, int DC, bool Causal, bool OutF16>
 __device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
     uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
-    uint32_t v_heads, half8_t (&qf)[Fast<D>::kQT][D / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
+    uint32_t v_heads, half8_t (&qf)[Fast<D>::kQT][DC / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
   constexpr int kQT = Fast<D>::kQT, kKT = Fast<D>::kKT, kHalves = Fast<D>::kHalves;
   constexpr uint32_t kKeys = Fast<D>::kKeys;
   constexpr uint32_t kQPW = Fast<D>::kQueriesPerWave, kQPB = Fast<D>::kQueriesPerBlock;
-  constexpr uint32_t kKS = D / 32;  // k steps (32 columns) of the score MFMAs
-  constexpr uint32_t kDT = D / 16;  // output d tiles (16 columns)
+  static_assert(DC % 32 == 0 && DC <= D, "computed columns: whole k steps of the tile");
+  constexpr uint32_t kKS = DC / 32;  // k steps (32 columns) of the score MFMAs
+  constexpr uint32_t kDT = DC / 16;  // output d tiles (16 columns)
   constexpr uint32_t kPairs = kKT * kKS;  // score MFMA groups (every query tile) per key block
   constexpr uint32_t kRB = KvTile<D>::kRowBytes;
   constexpr uint32_t kTile = KvTile<D>::kBytes;
@@ -332,8 +333,9 @@ __device__ __forceinline__ void attention_block(
     for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) s[kt][qt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    // Fragments two pairs ahead.
-    constexpr uint32_t kAhead = 2;
+    // Fragments two groups ahead (one for the 96-column tiles, which spill
+    // past 256 registers with two).
+    constexpr uint32_t kAhead = kQT == 2 && kKS == 3 ? 1 : 2;
     half8_t kf[kAhead], vf[kAhead];
 #pragma unroll
     for (uint32_t p = 0; p < kAhead; ++p) {
@@ -516,7 +518,7 @@ __device__ __forceinline__ void attention_block(
   if (kbi < nblocks) step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
   // V of the last block (and every DMA) has landed after this barrier.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  if (chain) load_q<D>(qf, query, stream, next_qb, query_rows, width, q_heads);
+  if (chain) load_q<D, DC>(qf, query, stream, next_qb, query_rows, width, q_heads);
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
   // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
@@ -553,7 +555,7 @@ __device__ __forceinline__ void attention_block(
 // without a load latency (and without the burst of loads that workgroups
 // starting together would issue).  Workgroups are remapped so each XCD
 // (round-robin dispatch over 8) runs whole streams, sharing K and V in its L2.
-template <int D, bool Causal, bool OutF16>
+template <int D, int DC, bool Causal, bool OutF16>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
@@ -573,8 +575,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   };
   const uint32_t pos0 = i * kBlocksPerGroup;
   const uint32_t reps = qblocks - pos0 < kBlocksPerGroup ? qblocks - pos0 : kBlocksPerGroup;
-  half8_t qf[Fast<D>::kQT][D / 32];
-  load_q<D>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
+  half8_t qf[Fast<D>::kQT][DC / 32];
+  load_q<D, DC>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
   bool loaded = false;  // this block's first K tile and Q fragments were fetched by the last one
   for (uint32_t rep = 0; rep < reps; ++rep) {
     // Every wave is done with the LDS stages before the next block's DMA.
@@ -583,8 +585,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     // A block with an even key block count ends in stage 1, so its last
     // step can fetch the next block's first K tile into stage 0.
     const bool chain = rep + 1 < reps && key_blocks<D, Causal>(qb, query_rows, key_rows) % 2 == 0;
-    if (rep > 0 && !loaded) load_q<D>(qf, query, stream, qb, query_rows, width, q_heads);
-    attention_block<D, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
+    if (rep > 0 && !loaded) load_q<D, DC>(qf, query, stream, qb, query_rows, width, q_heads);
+    attention_block<D, DC, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
                                        width, scale_log2, q_heads, k_heads, v_heads, qf, loaded,
                                        chain, qb_at(pos0 + rep + 1));
     loaded = chain;
@@ -862,26 +864,28 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
   }
 }
 
-template <int D, bool Causal, bool OutF16>
+template <int D, int DC, bool Causal, bool OutF16>
 int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock;
   const uint32_t qblocks = (a.query_rows + kQPB - 1) / kQPB;
   const uint64_t blocks = (uint64_t)((qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup) * a.streams;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL((attention_fwd_kernel<D, Causal, OutF16>), dim3((uint32_t)blocks),
+  hipLaunchKernelGGL((attention_fwd_kernel<D, DC, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
                      (const uint16_t*)a.key, (const uint16_t*)a.value, a.streams, a.query_rows,
                      a.key_rows, a.width, scale_log2, a.heads[0], a.heads[1], a.heads[2]);
   return hip_status(hipGetLastError());
 }
 
-template <int D>
+// Tile width D (LDS rows, DMA), computed columns DC (score k steps, output
+// tiles): the width rounded up to a multiple of 32.
+template <int D, int DC>
 int dispatch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   if (a.causal)
-    return a.output_f16 ? launch_fast<D, true, true>(stream, a, scale_log2)
-                        : launch_fast<D, true, false>(stream, a, scale_log2);
-  return a.output_f16 ? launch_fast<D, false, true>(stream, a, scale_log2)
-                      : launch_fast<D, false, false>(stream, a, scale_log2);
+    return a.output_f16 ? launch_fast<D, DC, true, true>(stream, a, scale_log2)
+                        : launch_fast<D, DC, true, false>(stream, a, scale_log2);
+  return a.output_f16 ? launch_fast<D, DC, false, true>(stream, a, scale_log2)
+                      : launch_fast<D, DC, false, false>(stream, a, scale_log2);
 }
 
 }  // namespace
@@ -901,12 +905,16 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
   const bool fits = ((uint64_t)a.key_rows + kMaxKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
   // Equal widths that are multiples of 8 up to 256 run in 64-, 128- or
-  // 256-wide tiles (zero padding); other widths take the MFMA kernel below,
-  // or the one-row-per-block kernel past its limits.
+  // 256-wide tiles (zero padding), computing 32, 64, 96, 128, 192 or 256
+  // columns; other widths take the MFMA kernel below, or the
+  // one-row-per-block kernel past its limits.
   if (aligned && fits && a.width == a.value_width && a.width % 8 == 0 && a.width <= 256) {
-    if (a.width > 128) return dispatch_fast<256>(stream, a, scale_log2);
-    return a.width > 64 ? dispatch_fast<128>(stream, a, scale_log2)
-                        : dispatch_fast<64>(stream, a, scale_log2);
+    if (a.width > 192) return dispatch_fast<256, 256>(stream, a, scale_log2);
+    if (a.width > 128) return dispatch_fast<256, 192>(stream, a, scale_log2);
+    if (a.width > 96) return dispatch_fast<128, 128>(stream, a, scale_log2);
+    if (a.width > 64) return dispatch_fast<128, 96>(stream, a, scale_log2);
+    if (a.width > 32) return dispatch_fast<64, 64>(stream, a, scale_log2);
+    return dispatch_fast<64, 32>(stream, a, scale_log2);
   }
   // Query/key width up to 256 and value width up to 512: the MFMA kernel for
   // other widths, in the smallest of its tile classes that holds them.

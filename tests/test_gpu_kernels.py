@@ -530,7 +530,7 @@ def test_attention_moving_reference_point(ipus, oracle, ctx, causal, streams, s,
     assert fp16_close(got, want, FP16_TOL)
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 192, 256])
 def test_attention_after_nan_filled_lds(ipus, oracle, ctx, d):
     """A GEMM over all-NaN operands first leaves NaN patterns in the LDS of
     every CU; the attention that follows must not pick any of them up (its
