@@ -7,17 +7,18 @@
 // crates/ipu-tests/src/diagnostic.rs:711-780 (key j allowed iff j <= i when
 // causal, 741-745; scale default 1/sqrt(width), 733-736).
 //
-// Fast kernel (width == value width, a multiple of 8 up to 256, computed in
-// tiles 64, 128 or 256 columns wide with zero padding):
+// Fast kernel (width == value width, a multiple of 8 up to 256, stored in
+// LDS tiles 64, 128 or 256 columns wide with zero padding; the MFMAs cover
+// the width rounded up to 32 columns):
 //   * 256 threads = 4 waves; a wave owns 32 queries (two tiles of 16; one
 //     tile at 256 columns), a workgroup 128 (64) queries of one stream; two
 //     workgroups share a CU (launch bound), so one SIMD runs the softmax of
 //     one wave while the MFMA pipe serves the other;
 //   * keys stream through LDS in blocks of 64 (32 at 256 columns) with two
-//     stages.  K and V tiles
-//     are copied global -> LDS with buffer_load ... lds (16 bytes per lane, no
-//     staging registers; rows past the end of the stream read as 0), both
-//     stored row-major [keys][D] with an XOR swizzle of 16-byte chunks;
+//     stages.  K and V tiles are copied global -> LDS with buffer_load ...
+//     lds (16 bytes per lane, no staging registers; rows past the end of the
+//     stream read as 0), both stored row-major [keys][D] with an XOR swizzle
+//     of 16-byte chunks;
 //   * v_mfma_f32_16x16x32_f16 throughout: under the board's power limit it
 //     sustains a higher clock than 32 x 32 x 16 on changing operands;
 //   * software pipeline: step j runs ONE MFMA cluster holding the scores of
