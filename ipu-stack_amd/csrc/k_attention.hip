@@ -37,7 +37,7 @@
 //     the score accumulator's key order;
 //   * each fragment read feeds one MFMA per query tile of the wave;
 //   * the reference point (running max) moves only when some probability of
-//     a block would exceed 2^kRescaleSlack, which the block's probability
+//     a block would exceed kSumLimit (2^8), which the block's probability
 //     sum bounds, so no max over the scores is taken on the common path:
 //     the result is exact for any reference point, and most blocks skip the
 //     max, the rescale of the output accumulators and the lane exchanges;
@@ -417,7 +417,7 @@ __device__ __forceinline__ void attention_block(
     }
     // Probabilities against the current reference points, and this lane's
     // share of each query's block sum: the fp16 probabilities that the MFMA
-    // consumes, added in pairs and quads in fp16 (each p <= 2^kRescaleSlack
+    // consumes, added in pairs and quads in fp16 (each p <= kSumLimit (2^8)
     // on the accepted path, so a quad sum stays far inside the fp16 range
     // and carries at most two roundings), then accumulated in fp32 by v_dot2.
     auto exps = [&](const float* neg_m, half8_t (*pf)[kQT], float* sum) __attribute__((always_inline)) {
@@ -437,8 +437,8 @@ __device__ __forceinline__ void attention_block(
       }
     };
     // A reference point moves only when some probability would exceed
-    // 2^kRescaleSlack, found without a max over the scores: every p is at
-    // most its lane's block sum, so sums <= 2^kRescaleSlack accept the block
+    // kSumLimit (2^8), found without a max over the scores: every p is at
+    // most its lane's block sum, so sums <= kSumLimit (2^8) accept the block
     // (overflow to inf and NaN, as against the -inf start, fail the test).
     // Otherwise each query's max over the block's keys (the four lanes that hold
     // it, so they share one reference point; finite, as every processed block
