@@ -523,26 +523,67 @@ __device__ __forceinline__ void attention_block(
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
   // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
+  if constexpr (OutF16) {
 #pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    const float inv = 1.0f / sum_of_query(l_run[qt]);
-    if (qi[qt] < query_rows) {
-      const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * width;
+    for (int qt = 0; qt < kQT; ++qt) {
+      const float inv = 1.0f / sum_of_query(l_run[qt]);
+      if (qi[qt] < query_rows) {
+        const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * width;
 #pragma unroll
-      for (uint32_t dt = 0; dt < kDT; ++dt) {
-        const uint32_t d = dt * 16 + 4 * g4;
-        if (d >= width) continue;  // padding (width is a multiple of 8)
-        if constexpr (OutF16) {
+        for (uint32_t dt = 0; dt < kDT; ++dt) {
+          const uint32_t d = dt * 16 + 4 * g4;
+          if (d >= width) continue;  // padding (width is a multiple of 8)
           half4_t hv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][qt][e] * inv);
           *reinterpret_cast<half4_t*>((uint16_t*)out + row + d) = hv;
-        } else {
+        }
+      }
+    }
+  } else {
+    // fp32 rows go out through LDS: a lane holds 4 columns of one query per
+    // d tile, so storing straight from registers writes 64-byte pieces of 16
+    // rows per instruction; staged, every instruction writes whole 512-byte
+    // row runs.  Each wave stages a 16-query tile (kPassCols columns per
+    // pass) in its quarter of the two V stages, which every wave is done
+    // reading after this barrier (the K stages may hold the next block's
+    // prefetched tile).  Rows of kPassCols fp32, 16-byte chunk c of row r at
+    // chunk c ^ (r & 15): a write instruction's 16 rows land on distinct
+    // banks.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Lane indices made opaque here, so the staging addresses are computed
+    // now rather than before the key loop (where they would hold registers).
+    uint32_t lane_e = lane, r16_e = r16, g4_e = g4;
+    asm volatile("" : "+v"(lane_e), "+v"(r16_e), "+v"(g4_e));
+    constexpr uint32_t kPassCols = kTile / 128;  // 16 rows x kPassCols x 4 B = kTile / 2
+    constexpr uint32_t kRowChunks = kPassCols / 4;
+    constexpr uint32_t kPasses = (DC + kPassCols - 1) / kPassCols;
+    static_assert(kPassCols % 16 == 0 && kRowChunks <= 32, "whole d tiles per pass, 512-byte rows at most");
+    uint8_t* stage = (wave_s < 2 ? lds_v0 : lds_v1) + (wave_s % 2) * (kTile / 2);
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      const float inv = 1.0f / sum_of_query(l_run[qt]);
+#pragma unroll
+      for (uint32_t pass = 0; pass < kPasses; ++pass) {
+#pragma unroll
+        for (uint32_t dt = pass * kPassCols / 16; dt < kDT && dt < (pass + 1) * kPassCols / 16; ++dt) {
+          const uint32_t c = (dt - pass * kPassCols / 16) * 4 + g4_e;
           float4_t fv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) fv[e] = o[dt][qt][e] * inv;
-          *reinterpret_cast<float4_t*>((float*)out + row + d) = fv;
+          *reinterpret_cast<float4_t*>(stage + r16_e * kPassCols * 4 + ((c ^ (r16_e & 15)) << 4)) = fv;
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t k = 0; k < 16 * kRowChunks / kWave; ++k) {
+          const uint32_t v = k * kWave + lane_e, r = v / kRowChunks, c = v % kRowChunks;
+          const uint32_t q = wq0 + 16 * qt + r, col = pass * kPassCols + c * 4;
+          const float4_t fv = *reinterpret_cast<const float4_t*>(
+              stage + r * kPassCols * 4 + ((c ^ (r & 15)) << 4));
+          if (q < query_rows && col < width)  // width is a multiple of 8
+            *reinterpret_cast<float4_t*>((float*)out + ((uint64_t)stream * query_rows + q) * width + col) = fv;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
