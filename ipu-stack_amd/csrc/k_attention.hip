@@ -636,7 +636,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
 }
 
 // MFMA attention for the widths the fast kernel does not take: query/key
-// width up to 256 and value width up to 512, equal or not, multiples of 8
+// width and value width up to 512, equal or not, multiples of 8
 // or not.  256 threads = 4 waves of 16 queries (one 16-query tile each); a
 // workgroup runs 64 queries of one stream (the heaviest causal blocks first)
 // and shares each block of 32 keys through LDS: the K and V tiles of the
@@ -848,7 +848,7 @@ int launch(hipStream_t stream, const AttentionArgs& a, float scale_log2, bool ve
 }  // namespace wide
 
 // One 64-lane block per (stream, query row): the fallback for query/key
-// widths above 256 (any query/key width, value width up to 512).
+// widths above 512 (any query/key width, value width up to 512).
 // Online softmax over keys one at a time (dot products by wave reduction).
 constexpr uint32_t kGeneralMaxValuePerLane = 8;  // value width <= 512
 
@@ -958,13 +958,14 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
     if (a.width > 32) return dispatch_fast<64, 64>(stream, a, scale_log2);
     return dispatch_fast<64, 32>(stream, a, scale_log2);
   }
-  // Query/key width up to 256 and value width up to 512: the MFMA kernel for
-  // other widths, in the smallest of its tile classes that holds them.
-  if (a.width <= 256 && a.value_width <= 512) {
+  // Query/key and value widths up to 512: the MFMA kernel for other widths,
+  // in the smallest of its tile classes that holds them.
+  if (a.width <= 512 && a.value_width <= 512) {
     const bool vec8 = aligned && a.width % 8 == 0 && a.value_width % 8 == 0;
     if (a.width <= 128 && a.value_width <= 128) return wide::launch<128, 128>(stream, a, scale_log2, vec8);
-    if (a.value_width <= 256) return wide::launch<256, 256>(stream, a, scale_log2, vec8);
-    return wide::launch<256, 512>(stream, a, scale_log2, vec8);
+    if (a.width <= 256 && a.value_width <= 256) return wide::launch<256, 256>(stream, a, scale_log2, vec8);
+    if (a.width <= 256) return wide::launch<256, 512>(stream, a, scale_log2, vec8);
+    return wide::launch<512, 512>(stream, a, scale_log2, vec8);
   }
   if (a.value_width > 64 * kGeneralMaxValuePerLane) return IPUS_ERROR_UNAVAILABLE;
   const uint64_t blocks = (uint64_t)a.streams * a.query_rows;

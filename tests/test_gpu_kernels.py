@@ -459,23 +459,24 @@ def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
                                                 (3, 65, 1, 128, 8), (2, 130, 97, 37, 53),
                                                 (1, 200, 260, 200, 72), (2, 64, 64, 136, 136),
                                                 (1, 129, 300, 256, 256), (1, 70, 90, 120, 264),
-                                                (1, 40, 50, 300, 40)])
+                                                (1, 40, 50, 300, 40), (1, 70, 90, 512, 512),
+                                                (2, 33, 40, 384, 128), (1, 20, 30, 520, 64)])
 def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d, dv):
     """Widths the fast kernel does not take (value width different from the
     query width, widths not a multiple of 8) run on the MFMA kernel for other
-    widths (query/key width up to 256, value width up to 512), and query/key
-    widths above 256 on the one-row-per-block kernel; equal widths that are
+    widths (query/key and value widths up to 512), and query/key widths
+    above 512 on the one-row-per-block kernel; equal widths that are
     multiples of 8 up to 256 here run the fast kernel's 256-wide tiles."""
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal)
     assert fp16_close(got, want, FP16_TOL)
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120)])
+@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120), (512, 512)])
 def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal, d, dv):
-    """Widths 136 and 256 (the fast kernel's 256-wide tiles) and query width
-    136 with value width 120 (the MFMA kernel for other widths) at 16 streams
-    x 2048 rows, fp16 output, checked on sampled rows."""
+    """Widths 136 and 256 (the fast kernel's 256-wide tiles), query width
+    136 with value width 120 and width 512 (the MFMA kernel for other widths)
+    at 16 streams x 2048 rows, fp16 output, checked on sampled rows."""
     rows = [0, 1, 63, 64, 500, 1023, 1024, 2047, 2048 + 5, 16 * 2048 - 1, 7 * 2048 + 1300]
     got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, d, dv, causal,
                                out_f16=True, rows=rows)
