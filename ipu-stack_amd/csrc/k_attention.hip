@@ -96,12 +96,13 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HI
 // 256-byte rows).  They depend only on the row's low bits and change only
 // the low 4 bits of the chunk index, and a bank is fixed by the byte offset
 // modulo 256, so 512-byte rows (D = 256) see the 256-byte rows' pattern.
-template <int D>
+template <int D, int Keys>
 struct KvTile {
   static constexpr uint32_t kRowBytes = D * 2;
   static constexpr uint32_t kChunks = D / 8;
-  static constexpr uint32_t kBytes = Fast<D>::kKeys * D * 2;
+  static constexpr uint32_t kBytes = Keys * D * 2;
   static constexpr uint32_t kDma = kBytes / 16 / kThreads;  // DMA instructions per thread
+  static constexpr uint32_t kDmaRows = kThreads / kChunks;   // rows per DMA instruction
 };
 template <int D>
 __device__ __forceinline__ uint32_t k_swz(uint32_t row) {
@@ -145,7 +146,7 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 template <int D, bool IsK>
 __device__ __forceinline__ uint32_t kv_offset(uint32_t row_bytes, uint32_t width,
                                               uint32_t first_row = 0) {
-  const uint32_t row = threadIdx.x / KvTile<D>::kChunks, phys = threadIdx.x % KvTile<D>::kChunks;
+  const uint32_t row = threadIdx.x / (D / 8), phys = threadIdx.x % (D / 8);
   const uint32_t srow = row + first_row;
   const uint32_t chunk = phys ^ (IsK ? k_swz<D>(srow) : v_swz<D>(srow));
   return chunk * 8 < width ? row * row_bytes + chunk * 16 : kPadOffset;
@@ -191,29 +192,38 @@ __device__ __forceinline__ void load_q(half8_t (&qf)[Fast<D>::kQT][DC / 32], con
   }
 }
 
-template <int D, int DC, bool Causal, bool OutF16>
+// D / DC: K tile width and score columns (query/key width); DV / DVC: V
+// tile width and output columns (value width).  The block shape (query
+// tiles per wave, keys per block) follows the wider tile.
+template <int D, int DC, int DV, int DVC, bool Causal, bool OutF16>
 __device__ __forceinline__ void attention_block(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t stream, uint32_t qb, uint32_t query_rows,
-    uint32_t key_rows, uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
-    uint32_t v_heads, half8_t (&qf)[Fast<D>::kQT][DC / 32], bool k0_loaded, bool chain, uint32_t next_qb) {
-  constexpr int kQT = Fast<D>::kQT, kKT = Fast<D>::kKT, kHalves = Fast<D>::kHalves;
-  constexpr uint32_t kKeys = Fast<D>::kKeys;
-  constexpr uint32_t kQPW = Fast<D>::kQueriesPerWave, kQPB = Fast<D>::kQueriesPerBlock;
-  static_assert(DC % 32 == 0 && DC <= D, "computed columns: whole k steps of the tile");
-  constexpr uint32_t kKS = DC / 32;  // k steps (32 columns) of the score MFMAs
-  constexpr uint32_t kDT = DC / 16;  // output d tiles (16 columns)
-  constexpr uint32_t kPairs = kKT * kKS;  // score MFMA groups (every query tile) per key block
-  constexpr uint32_t kRB = KvTile<D>::kRowBytes;
-  constexpr uint32_t kTile = KvTile<D>::kBytes;
-  constexpr uint32_t kDmaRows = kThreads / KvTile<D>::kChunks;  // rows per DMA instruction
-  static_assert(kPairs == kHalves * kDT, "one output MFMA group per score MFMA group");
+    uint32_t key_rows, uint32_t width, uint32_t value_width, float scale_log2, uint32_t q_heads,
+    uint32_t k_heads, uint32_t v_heads, half8_t (&qf)[Fast<(D > DV ? D : DV)>::kQT][DC / 32],
+    bool k0_loaded, bool chain, uint32_t next_qb) {
+  using F = Fast<(D > DV ? D : DV)>;
+  constexpr int kQT = F::kQT, kKT = F::kKT, kHalves = F::kHalves;
+  constexpr uint32_t kKeys = F::kKeys;
+  constexpr uint32_t kQPW = F::kQueriesPerWave, kQPB = F::kQueriesPerBlock;
+  static_assert(DC % 32 == 0 && DC <= D, "score columns: whole k steps of the tile");
+  static_assert(DVC % 16 == 0 && DVC <= DV, "output columns: whole d tiles of the tile");
+  constexpr uint32_t kKS = DC / 32;   // k steps (32 columns) of the score MFMAs
+  constexpr uint32_t kDT = DVC / 16;  // output d tiles (16 columns)
+  constexpr uint32_t kScoreGroups = kKT * kKS;   // score MFMA groups (every query tile) per block
+  constexpr uint32_t kOutGroups = kHalves * kDT;  // output MFMA groups per block
+  constexpr uint32_t kPairs = kScoreGroups > kOutGroups ? kScoreGroups : kOutGroups;
+  using KT = KvTile<D, kKeys>;
+  using VT = KvTile<DV, kKeys>;
+  constexpr uint32_t kRB = KT::kRowBytes, kVRB = VT::kRowBytes;
+  constexpr uint32_t kTile = KT::kBytes, kVTile = VT::kBytes;
+  constexpr uint32_t kDmaRows = KT::kDmaRows, kVDmaRows = VT::kDmaRows;
   // Two stages, each a distinct LDS object so the compiler can see that the
   // DMA into one stage never aliases the fragment reads of the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTile];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kVTile];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTile];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kVTile];
 
   const uint32_t q0 = qb * kQPB;
   const uint32_t lane = threadIdx.x % kWave;
@@ -222,22 +232,24 @@ __device__ __forceinline__ void attention_block(
   const uint32_t wq0 = q0 + wave_s * kQPW;  // first query of this wave
 
   // Stream s of an operand with h heads is head s % h of matrix s / h of a
-  // [streams / h, rows, h * D] tensor (h = 1: contiguous [streams, rows, D]).
-  // The tile width D is the stream width padded to 64 or 128.
-  const uint32_t k_row_bytes = k_heads * width * 2u, v_row_bytes = v_heads * width * 2u;
+  // [streams / h, rows, h * w] tensor (h = 1: contiguous [streams, rows, w];
+  // w the operand's width).  The tile widths are the widths padded to 64,
+  // 128 or 256.
+  const uint32_t k_row_bytes = k_heads * width * 2u, v_row_bytes = v_heads * value_width * 2u;
   const uint16_t* K = key + (uint64_t)(stream / k_heads) * key_rows * k_heads * width + (stream % k_heads) * width;
-  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * width + (stream % v_heads) * width;
+  const uint16_t* V = value + (uint64_t)(stream / v_heads) * key_rows * v_heads * value_width +
+                      (stream % v_heads) * value_width;
   const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)K, 0, (int)((key_rows - 1) * k_row_bytes + width * 2u), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + width * 2u), kBufferFlags);
+      (void*)V, 0, (int)((key_rows - 1) * v_row_bytes + value_width * 2u), kBufferFlags);
   // K chunks of even and odd DMA instructions (they differ only at D = 256).
   const uint32_t k_voff = kv_offset<D, true>(k_row_bytes, width);
   const uint32_t k_voff_odd = kDmaRows % 16 == 0 ? k_voff : kv_offset<D, true>(k_row_bytes, width, kDmaRows);
-  const uint32_t v_voff = kv_offset<D, false>(v_row_bytes, width);
-  static_assert(kDmaRows % 8 == 0, "the V swizzle depends on row bits 0-2 only");
+  const uint32_t v_voff = kv_offset<DV, false>(v_row_bytes, value_width);
+  static_assert(kVDmaRows % 8 == 0, "the V swizzle depends on row bits 0-2 only");
 
-  const uint32_t nblocks = key_blocks<D, Causal>(qb, query_rows, key_rows);
+  const uint32_t nblocks = key_blocks<(D > DV ? D : DV), Causal>(qb, query_rows, key_rows);
   const uint32_t k_block_bytes = kKeys * k_row_bytes;
   const uint32_t v_block_bytes = kKeys * v_row_bytes;
   // Blocks this wave computes scores for (causal: keys <= its last query).
@@ -287,7 +299,7 @@ __device__ __forceinline__ void attention_block(
   uint32_t vbase;
   {
     const uint32_t row = 4 * g4 + r16 / 4, c1 = (r16 % 4) / 2;
-    vbase = row * kRB + ((c1 ^ v_swz<D>(row)) << 4) + 8 * (r16 % 2);
+    vbase = row * kVRB + ((c1 ^ v_swz<DV>(row)) << 4) + 8 * (r16 % 2);
   }
   uint32_t kofs[kKS], vofs[kDT];
 #pragma unroll
@@ -299,9 +311,9 @@ __device__ __forceinline__ void attention_block(
     return __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(p));
   };
   auto vfrag = [&](const uint8_t* lv, uint32_t dt, uint32_t kk) __attribute__((always_inline)) {
-    const uint8_t* p = lv + vofs[dt] + 32 * kk * kRB;
+    const uint8_t* p = lv + vofs[dt] + 32 * kk * kVRB;
     const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)p);
-    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kRB));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS short4_t*)(p + 16 * kVRB));
     return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
@@ -315,7 +327,7 @@ __device__ __forceinline__ void attention_block(
     dma16(k_rsrc, nk + (i * kThreads + wave_s * kWave) * 16, (i % 2 ? k_voff_odd : k_voff) + so);
   };
   auto dma_v = [&](uint32_t i, uint8_t* nv, uint32_t bytes) __attribute__((always_inline)) {
-    uint32_t so = bytes + i * kDmaRows * v_row_bytes;
+    uint32_t so = bytes + i * kVDmaRows * v_row_bytes;
     asm volatile("" : "+s"(so));
     dma16(v_rsrc, nv + (i * kThreads + wave_s * kWave) * 16, v_voff + so);
   };
@@ -340,8 +352,9 @@ __device__ __forceinline__ void attention_block(
     half8_t kf[kAhead], vf[kAhead];
 #pragma unroll
     for (uint32_t p = 0; p < kAhead; ++p) {
-      kf[p] = kfrag(lk, p % kKT, p / kKT);
-      if constexpr (WithPv) vf[p] = vfrag(lv, p % kDT, p / kDT);
+      if (p < kScoreGroups) kf[p] = kfrag(lk, p % kKT, p / kKT);
+      if constexpr (WithPv)
+        if (p < kOutGroups) vf[p] = vfrag(lv, p % kDT, p / kDT);
     }
     __builtin_amdgcn_sched_barrier(0);
     // Raised priority while this wave feeds the matrix pipe: the other wave
@@ -352,21 +365,22 @@ __device__ __forceinline__ void attention_block(
       const uint32_t ks = p / kKT, kt = p % kKT, kk = p / kDT, dt = p % kDT;
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
-        s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[p % kAhead], qf[qt][ks], s[kt][qt], 0, 0, 0);
+        if (p < kScoreGroups)
+          s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[p % kAhead], qf[qt][ks], s[kt][qt], 0, 0, 0);
         if constexpr (WithPv)
-          o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[p % kAhead], pp[kk][qt], o[dt][qt], 0, 0, 0);
+          if (p < kOutGroups)
+            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[p % kAhead], pp[kk][qt], o[dt][qt], 0, 0, 0);
       }
-      if (p + kAhead < kPairs) {
-        kf[p % kAhead] = kfrag(lk, (p + kAhead) % kKT, (p + kAhead) / kKT);
-        if constexpr (WithPv) vf[p % kAhead] = vfrag(lv, (p + kAhead) % kDT, (p + kAhead) / kDT);
-      }
-      // DMA instructions spread over the pairs: K tile first, then V.
-      constexpr uint32_t kDmaPer = (2 * KvTile<D>::kDma + kPairs - 1) / kPairs;
+      if (p + kAhead < kScoreGroups) kf[p % kAhead] = kfrag(lk, (p + kAhead) % kKT, (p + kAhead) / kKT);
+      if constexpr (WithPv)
+        if (p + kAhead < kOutGroups) vf[p % kAhead] = vfrag(lv, (p + kAhead) % kDT, (p + kAhead) / kDT);
+      // DMA instructions spread over the groups: K tile first, then V.
+      constexpr uint32_t kDmaPer = (KT::kDma + VT::kDma + kPairs - 1) / kPairs;
 #pragma unroll
       for (uint32_t u = 0; u < kDmaPer; ++u) {
         const uint32_t i = p * kDmaPer + u;
-        if (i < KvTile<D>::kDma) dma_k(i, nk, next * k_block_bytes);
-        else if (i < 2 * KvTile<D>::kDma) dma_v(i - KvTile<D>::kDma, nv, kbi * v_block_bytes);
+        if (i < KT::kDma) dma_k(i, nk, next * k_block_bytes);
+        else if (i < KT::kDma + VT::kDma) dma_v(i - KT::kDma, nv, kbi * v_block_bytes);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -504,10 +518,10 @@ __device__ __forceinline__ void attention_block(
   // next block, its Q fragments are loaded once this block's last scores
   // are done with them.
 #pragma unroll
-  for (uint32_t i = 0; i < KvTile<D>::kDma; ++i)
+  for (uint32_t i = 0; i < KT::kDma; ++i)
     if (!k0_loaded) dma_k(i, lds_k0, 0);
 #pragma unroll
-  for (uint32_t i = 0; i < kTile / 16 / kThreads; ++i)
+  for (uint32_t i = 0; i < kVTile / 16 / kThreads; ++i)
     *reinterpret_cast<u32x4*>(lds_v1 + (i * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
   // Both steps of a pair run unconditionally, so the loop body is one
   // straight path; an odd last block runs after the loop.
@@ -519,7 +533,7 @@ __device__ __forceinline__ void attention_block(
   if (kbi < nblocks) step(lds_k0, lds_v1, lds_k1, lds_v0, kbi);
   // V of the last block (and every DMA) has landed after this barrier.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  if (chain) load_q<D, DC>(qf, query, stream, next_qb, query_rows, width, q_heads);
+  if (chain) load_q<(D > DV ? D : DV), DC>(qf, query, stream, next_qb, query_rows, width, q_heads);
   if (nproc == nblocks) pv_only((nblocks - 1) % 2 == 0 ? lds_v0 : lds_v1);
 
   // o[dt][qt][e] = O^T[d = 16 dt + 4 (l / 16) + e][qi[qt]], unnormalised.
@@ -528,11 +542,11 @@ __device__ __forceinline__ void attention_block(
     for (int qt = 0; qt < kQT; ++qt) {
       const float inv = 1.0f / sum_of_query(l_run[qt]);
       if (qi[qt] < query_rows) {
-        const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * width;
+        const uint64_t row = ((uint64_t)stream * query_rows + qi[qt]) * value_width;
 #pragma unroll
         for (uint32_t dt = 0; dt < kDT; ++dt) {
           const uint32_t d = dt * 16 + 4 * g4;
-          if (d >= width) continue;  // padding (width is a multiple of 8)
+          if (d >= value_width) continue;  // padding (a multiple of 8)
           half4_t hv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) hv[e] = (half_t)(o[dt][qt][e] * inv);
@@ -555,11 +569,11 @@ __device__ __forceinline__ void attention_block(
     // now rather than before the key loop (where they would hold registers).
     uint32_t lane_e = lane, r16_e = r16, g4_e = g4;
     asm volatile("" : "+v"(lane_e), "+v"(r16_e), "+v"(g4_e));
-    constexpr uint32_t kPassCols = kTile / 128;  // 16 rows x kPassCols x 4 B = kTile / 2
+    constexpr uint32_t kPassCols = kVTile / 128;  // 16 rows x kPassCols x 4 B = kVTile / 2
     constexpr uint32_t kRowChunks = kPassCols / 4;
-    constexpr uint32_t kPasses = (DC + kPassCols - 1) / kPassCols;
+    constexpr uint32_t kPasses = (DVC + kPassCols - 1) / kPassCols;
     static_assert(kPassCols % 16 == 0 && kRowChunks <= 32, "whole d tiles per pass, 512-byte rows at most");
-    uint8_t* stage = (wave_s < 2 ? lds_v0 : lds_v1) + (wave_s % 2) * (kTile / 2);
+    uint8_t* stage = (wave_s < 2 ? lds_v0 : lds_v1) + (wave_s % 2) * (kVTile / 2);
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
       const float inv = 1.0f / sum_of_query(l_run[qt]);
@@ -580,8 +594,8 @@ __device__ __forceinline__ void attention_block(
           const uint32_t q = wq0 + 16 * qt + r, col = pass * kPassCols + c * 4;
           const float4_t fv = *reinterpret_cast<const float4_t*>(
               stage + r * kPassCols * 4 + ((c ^ (r & 15)) << 4));
-          if (q < query_rows && col < width)  // width is a multiple of 8
-            *reinterpret_cast<float4_t*>((float*)out + ((uint64_t)stream * query_rows + q) * width + col) = fv;
+          if (q < query_rows && col < value_width)  // a multiple of 8
+            *reinterpret_cast<float4_t*>((float*)out + ((uint64_t)stream * query_rows + q) * value_width + col) = fv;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -597,12 +611,14 @@ __device__ __forceinline__ void attention_block(
 // without a load latency (and without the burst of loads that workgroups
 // starting together would issue).  Workgroups are remapped so each XCD
 // (round-robin dispatch over 8) runs whole streams, sharing K and V in its L2.
-template <int D, int DC, bool Causal, bool OutF16>
+template <int D, int DC, int DV, int DVC, bool Causal, bool OutF16>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     void* __restrict__ out, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, uint32_t streams, uint32_t query_rows, uint32_t key_rows,
-    uint32_t width, float scale_log2, uint32_t q_heads, uint32_t k_heads, uint32_t v_heads) {
-  constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock;
+    uint32_t width, uint32_t value_width, float scale_log2, uint32_t q_heads, uint32_t k_heads,
+    uint32_t v_heads) {
+  constexpr int W = D > DV ? D : DV;
+  constexpr uint32_t kQPB = Fast<W>::kQueriesPerBlock;
   const uint32_t qblocks = (query_rows + kQPB - 1) / kQPB;
   const uint32_t per_stream = (qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup;
   const uint32_t total = per_stream * streams;
@@ -617,8 +633,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   };
   const uint32_t pos0 = i * kBlocksPerGroup;
   const uint32_t reps = qblocks - pos0 < kBlocksPerGroup ? qblocks - pos0 : kBlocksPerGroup;
-  half8_t qf[Fast<D>::kQT][DC / 32];
-  load_q<D, DC>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
+  half8_t qf[Fast<W>::kQT][DC / 32];
+  load_q<W, DC>(qf, query, stream, qb_at(pos0), query_rows, width, q_heads);
   bool loaded = false;  // this block's first K tile and Q fragments were fetched by the last one
   for (uint32_t rep = 0; rep < reps; ++rep) {
     // Every wave is done with the LDS stages before the next block's DMA.
@@ -626,11 +642,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     const uint32_t qb = qb_at(pos0 + rep);
     // A block with an even key block count ends in stage 1, so its last
     // step can fetch the next block's first K tile into stage 0.
-    const bool chain = rep + 1 < reps && key_blocks<D, Causal>(qb, query_rows, key_rows) % 2 == 0;
-    if (rep > 0 && !loaded) load_q<D, DC>(qf, query, stream, qb, query_rows, width, q_heads);
-    attention_block<D, DC, Causal, OutF16>(out, query, key, value, stream, qb, query_rows, key_rows,
-                                       width, scale_log2, q_heads, k_heads, v_heads, qf, loaded,
-                                       chain, qb_at(pos0 + rep + 1));
+    const bool chain = rep + 1 < reps && key_blocks<W, Causal>(qb, query_rows, key_rows) % 2 == 0;
+    if (rep > 0 && !loaded) load_q<W, DC>(qf, query, stream, qb, query_rows, width, q_heads);
+    attention_block<D, DC, DV, DVC, Causal, OutF16>(out, query, key, value, stream, qb, query_rows,
+                                                    key_rows, width, value_width, scale_log2, q_heads,
+                                                    k_heads, v_heads, qf, loaded, chain,
+                                                    qb_at(pos0 + rep + 1));
     loaded = chain;
   }
 }
@@ -906,28 +923,29 @@ __global__ __launch_bounds__(64) void attention_general_kernel(
   }
 }
 
-template <int D, int DC, bool Causal, bool OutF16>
+template <int D, int DC, int DV, int DVC, bool Causal, bool OutF16>
 int launch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
-  constexpr uint32_t kQPB = Fast<D>::kQueriesPerBlock;
+  constexpr uint32_t kQPB = Fast<(D > DV ? D : DV)>::kQueriesPerBlock;
   const uint32_t qblocks = (a.query_rows + kQPB - 1) / kQPB;
   const uint64_t blocks = (uint64_t)((qblocks + kBlocksPerGroup - 1) / kBlocksPerGroup) * a.streams;
   if (blocks > 0x7fffffffu) return IPUS_ERROR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL((attention_fwd_kernel<D, DC, Causal, OutF16>), dim3((uint32_t)blocks),
+  hipLaunchKernelGGL((attention_fwd_kernel<D, DC, DV, DVC, Causal, OutF16>), dim3((uint32_t)blocks),
                      dim3(kThreads), 0, stream, a.out, (const uint16_t*)a.query,
                      (const uint16_t*)a.key, (const uint16_t*)a.value, a.streams, a.query_rows,
-                     a.key_rows, a.width, scale_log2, a.heads[0], a.heads[1], a.heads[2]);
+                     a.key_rows, a.width, a.value_width, scale_log2, a.heads[0], a.heads[1],
+                     a.heads[2]);
   return hip_status(hipGetLastError());
 }
 
-// Tile width D (LDS rows, DMA), computed columns DC (score k steps, output
-// tiles): the width rounded up to a multiple of 32.
-template <int D, int DC>
+// Tile widths D / DV (LDS rows, DMA) and computed columns DC / DVC (score
+// k steps / output tiles) of the query-key and value widths.
+template <int D, int DC, int DV = D, int DVC = DC>
 int dispatch_fast(hipStream_t stream, const AttentionArgs& a, float scale_log2) {
   if (a.causal)
-    return a.output_f16 ? launch_fast<D, DC, true, true>(stream, a, scale_log2)
-                        : launch_fast<D, DC, true, false>(stream, a, scale_log2);
-  return a.output_f16 ? launch_fast<D, DC, false, true>(stream, a, scale_log2)
-                      : launch_fast<D, DC, false, false>(stream, a, scale_log2);
+    return a.output_f16 ? launch_fast<D, DC, DV, DVC, true, true>(stream, a, scale_log2)
+                        : launch_fast<D, DC, DV, DVC, true, false>(stream, a, scale_log2);
+  return a.output_f16 ? launch_fast<D, DC, DV, DVC, false, true>(stream, a, scale_log2)
+                      : launch_fast<D, DC, DV, DVC, false, false>(stream, a, scale_log2);
 }
 
 }  // namespace
@@ -944,7 +962,8 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
   // The fast kernel addresses one stream's K or V through a buffer
   // descriptor with a 31-bit byte range; the offsets of the last block's
   // rows (up to 63 past the end) and of padding chunks stay below 2^32.
-  const uint64_t kv_pitch = (uint64_t)(a.heads[1] > a.heads[2] ? a.heads[1] : a.heads[2]) * a.width * 2;
+  const uint64_t k_pitch = (uint64_t)a.heads[1] * a.width * 2, v_pitch = (uint64_t)a.heads[2] * a.value_width * 2;
+  const uint64_t kv_pitch = k_pitch > v_pitch ? k_pitch : v_pitch;
   const bool fits = ((uint64_t)a.key_rows + kMaxKeysPerBlock) * kv_pitch <= 0x7fff0000ull;
   // Equal widths that are multiples of 8 up to 256 run in 64-, 128- or
   // 256-wide tiles (zero padding), computing 32, 64, 96, 128, 192 or 256
@@ -957,6 +976,17 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
     if (a.width > 64) return dispatch_fast<128, 96>(stream, a, scale_log2);
     if (a.width > 32) return dispatch_fast<64, 64>(stream, a, scale_log2);
     return dispatch_fast<64, 32>(stream, a, scale_log2);
+  }
+  // Unequal widths, multiples of 8, whose tile widths (64, 128 or 256 each)
+  // are one of these pairs: the same kernel with separate K and V tiles.
+  if (aligned && fits && a.width % 8 == 0 && a.value_width % 8 == 0 && a.width <= 256 &&
+      a.value_width <= 256) {
+    auto tile = [](uint32_t w) { return w <= 64 ? 64u : w <= 128 ? 128u : 256u; };
+    const uint32_t tq = tile(a.width), tv = tile(a.value_width);
+    if (tq == 128 && tv == 64) return dispatch_fast<128, 128, 64, 64>(stream, a, scale_log2);
+    if (tq == 64 && tv == 128) return dispatch_fast<64, 64, 128, 128>(stream, a, scale_log2);
+    if (tq == 256 && tv == 128) return dispatch_fast<256, 256, 128, 128>(stream, a, scale_log2);
+    if (tq == 128 && tv == 256) return dispatch_fast<128, 128, 256, 256>(stream, a, scale_log2);
   }
   // Query/key and value widths up to 512: the MFMA kernel for other widths,
   // in the smallest of its tile classes that holds them.

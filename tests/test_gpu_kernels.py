@@ -460,23 +460,30 @@ def test_attention_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d):
                                                 (1, 200, 260, 200, 72), (2, 64, 64, 136, 136),
                                                 (1, 129, 300, 256, 256), (1, 70, 90, 120, 264),
                                                 (1, 40, 50, 300, 40), (1, 70, 90, 512, 512),
-                                                (2, 33, 40, 384, 128), (1, 20, 30, 520, 64)])
+                                                (2, 33, 40, 384, 128), (1, 20, 30, 520, 64),
+                                                (2, 300, 300, 128, 64), (1, 129, 200, 192, 128),
+                                                (2, 100, 64, 64, 128), (1, 80, 96, 128, 256),
+                                                (1, 150, 150, 256, 136)])
 def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq, sk, d, dv):
-    """Widths the fast kernel does not take (value width different from the
-    query width, widths not a multiple of 8) run on the MFMA kernel for other
-    widths (query/key and value widths up to 512), and query/key widths
-    above 512 on the one-row-per-block kernel; equal widths that are
-    multiples of 8 up to 256 here run the fast kernel's 256-wide tiles."""
+    """Widths the fast kernel does not take (widths not a multiple of 8,
+    unequal widths whose tiles are not one of its pairs) run on the MFMA
+    kernel for other widths (query/key and value widths up to 512), and
+    query/key widths above 512 on the one-row-per-block kernel; equal widths
+    up to 256 and the tile pairs 128/64, 64/128, 256/128 and 128/256 here
+    run the fast kernel."""
     got, want = attention_case(ipus, oracle, ctx, streams, sq, sk, d, dv, causal)
     assert fp16_close(got, want, FP16_TOL)
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120), (512, 512)])
+@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120), (512, 512), (128, 64),
+                                  (192, 128)])
 def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal, d, dv):
     """Widths 136 and 256 (the fast kernel's 256-wide tiles), query width
-    136 with value width 120 and width 512 (the MFMA kernel for other widths)
-    at 16 streams x 2048 rows, fp16 output, checked on sampled rows."""
+    136 with value width 120 and width 512 (the MFMA kernel for other
+    widths), query/value widths 128/64 and 192/128 (the fast kernel's
+    separate K and V tiles) at 16 streams x 2048 rows, fp16 output, checked
+    on sampled rows."""
     rows = [0, 1, 63, 64, 500, 1023, 1024, 2047, 2048 + 5, 16 * 2048 - 1, 7 * 2048 + 1300]
     got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, d, dv, causal,
                                out_f16=True, rows=rows)
@@ -598,6 +605,30 @@ def test_attention_heads_view_equals_split_copy(ipus, oracle, ctx, causal, batch
     got = run(ctx, "ipu_stack_flash_attention_heads_f16", streams * s * d * 4, [qx, ks, vx],
               common + [heads, 1, heads], np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("batch,heads,s,d,dv", [(2, 2, 128, 128, 64), (1, 3, 70, 64, 128),
+                                                (1, 2, 100, 192, 128)])
+def test_attention_heads_view_uneven_widths(ipus, oracle, ctx, causal, batch, heads, s, d, dv):
+    """Strided heads with a value width other than the query width: the
+    value's head pitch is heads * dv.  Bit-identical to the contiguous launch
+    on split copies."""
+    streams = batch * heads
+    qx = synth(ipus, batch * s * heads * d, 62, 1, 1).reshape(batch, s, heads * d)
+    kx = synth(ipus, batch * s * heads * d, 62, 2, 1).reshape(batch, s, heads * d)
+    vx = synth(ipus, batch * s * heads * dv, 62, 3, 1).reshape(batch, s, heads * dv)
+    qs, ks, vs = (oracle.f32_to_f16(oracle.split_heads(oracle.f16_to_f32(t), heads))
+                  for t in (qx, kx, vx))
+    common = [streams, s, s, d, dv, 0, int(causal), 0]
+    want = run(ctx, "ipu_stack_flash_attention_online_f16", streams * s * dv * 4, [qs, ks, vs],
+               common, np.float32)
+    got = run(ctx, "ipu_stack_flash_attention_heads_f16", streams * s * dv * 4, [qx, kx, vx],
+              common + [heads, heads, heads], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = oracle.attention(oracle.f16_to_f32(qs), oracle.f16_to_f32(ks), oracle.f16_to_f32(vs),
+                           streams, s, s, d, dv, causal, None)
+    assert fp16_close(want.reshape(-1, dv), ref, FP16_TOL)
 
 
 def test_attention_heads_view_rejects_uneven_heads(ipus, ctx):
