@@ -677,8 +677,9 @@ LEGS = ("mfma_calibration", "gemm_f16_layouts", "gemm_f32_4096", "attention_caus
 def bench_off_fast_path(ipus, ctx, steps):
     """Shapes no BASELINE config uses, on the kernels' other paths: fp16 /
     fp32 GEMMs whose pitches are not multiples of 8 / 4 (element-gathering
-    tile kernels), attention at width 256 (the fast kernel's 256-wide tiles)
-    and at value width 64 beside query width 128 (the MFMA kernel for uneven
+    tile kernels), attention at width 256 (the fast kernel's 256-wide
+    tiles), at value width 64 beside query width 128 (its separate K and V
+    tiles) and at query / value widths 136 / 120 (the MFMA kernel for other
     widths)."""
     out = {}
 
@@ -711,6 +712,7 @@ def bench_off_fast_path(ipus, ctx, steps):
     gemm("gemm_f32_4096x4096x4097", 4096, 4096, 4097, True)
     attention("attention_16x2048_d256", 16, 2048, 256, 256)
     attention("attention_16x2048_d128_dv64", 16, 2048, 128, 64)
+    attention("attention_16x2048_d136_dv120", 16, 2048, 136, 120)
     return out
 
 
