@@ -7,9 +7,10 @@
 // crates/ipu-tests/src/diagnostic.rs:711-780 (key j allowed iff j <= i when
 // causal, 741-745; scale default 1/sqrt(width), 733-736).
 //
-// Fast kernel (width == value width, a multiple of 8 up to 256, stored in
-// LDS tiles 64, 128 or 256 columns wide with zero padding; the MFMAs cover
-// the width rounded up to 32 columns):
+// Fast kernel (query/key and value widths multiples of 8 up to 256, equal
+// or with tiles 128/64, 64/128, 256/128 or 128/256; stored in LDS tiles 64,
+// 128 or 256 columns wide with zero padding; for equal widths the MFMAs
+// cover the width rounded up to 32 columns):
 //   * 256 threads = 4 waves; a wave owns 32 queries (two tiles of 16; one
 //     tile at 256 columns), a workgroup 128 (64) queries of one stream; two
 //     workgroups share a CU (launch bound), so one SIMD runs the softmax of
