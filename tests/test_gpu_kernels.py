@@ -476,14 +476,13 @@ def test_attention_general_kernel_shapes(ipus, oracle, ctx, causal, streams, sq,
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (136, 120), (512, 512), (128, 64),
-                                  (192, 128)])
+@pytest.mark.parametrize("d,dv", [(136, 136), (256, 256), (132, 132), (512, 512), (128, 64),
+                                  (136, 120)])
 def test_attention_wide_heads_sampled_rows(ipus, oracle, ctx, causal, d, dv):
-    """Widths 136 and 256 (the fast kernel's 256-wide tiles), query width
-    136 with value width 120 and width 512 (the MFMA kernel for other
-    widths), query/value widths 128/64 and 192/128 (the fast kernel's
-    separate K and V tiles) at 16 streams x 2048 rows, fp16 output, checked
-    on sampled rows."""
+    """Widths 136 and 256 (the fast kernel's 256-wide tiles), query/value
+    widths 128/64 and 136/120 (its separate K and V tiles), widths 132 (not
+    a multiple of 8) and 512 (the MFMA kernel for other widths) at 16
+    streams x 2048 rows, fp16 output, checked on sampled rows."""
     rows = [0, 1, 63, 64, 500, 1023, 1024, 2047, 2048 + 5, 16 * 2048 - 1, 7 * 2048 + 1300]
     got, want = attention_case(ipus, oracle, ctx, 16, 2048, 2048, d, dv, causal,
                                out_f16=True, rows=rows)
