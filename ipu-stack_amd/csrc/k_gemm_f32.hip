@@ -9,11 +9,15 @@
 // alignments with bounds-checked element loads and stores):
 //   * block tile 128 x 128 x 32, 4 waves in a 2 x 2 grid, each wave 64 x 64
 //     as 2 x 2 MFMA tiles;
-//   * operands staged in LDS k-major ([k][m], [k][n]) so a fragment is 32
-//     consecutive floats of one k row; the 16-byte chunk index is XOR-swizzled
-//     by (k >> 2) & 7 so the transposing tile stores are conflict-free;
-//   * a K-contiguous operand (row-major A, transposed B) is transposed in
-//     registers on 4 x 4 blocks before its LDS store;
+//   * each operand is staged in LDS in the layout it has in memory, so no
+//     tile is transposed on the way: an operand whose x axis (m or n) is
+//     contiguous k-major ([k][x], 16-byte chunks XOR-swizzled by (k >> 2) &
+//     7), one whose k axis is contiguous x-major ([x][k], rows of 32 k,
+//     chunks XOR-swizzled by (x >> 1) & 7);
+//   * the k pair of MFMA substep p is (p, 16 + p) for lanes 0-31 and 32-63, a
+//     permutation of the step's 32 k that both operands share, so a lane reads
+//     four substeps' values of an x-major tile as one 16-byte chunk (k-major
+//     tiles: one element per substep);
 //   * one LDS stage (32 KiB, so three workgroups share a CU): the next K
 //     step's tiles load into registers during the MFMAs and are stored
 //     between two barriers (4096^3: 121 -> 126 TFLOP/s against two stages
@@ -33,9 +37,16 @@ constexpr int kTileBytes = kBK * kBM * 4;  // 16 KiB per operand tile
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? 0 : IPUS_ERROR_HIP_BASE - (int)e; }
 
-// Byte offset of element (k, x) in a [32][128] fp32 tile.
+// Byte offset of element (k, x) in a [32 k][128 x] fp32 tile (k-major,
+// the layout of an operand whose x axis is contiguous in memory).
 __device__ __forceinline__ uint32_t swz32(uint32_t k, uint32_t x) {
   return k * 512u + ((((x >> 2) ^ ((k >> 2) & 7u)) << 4) | ((x & 3u) << 2));
+}
+// Byte offset of 16-byte chunk c (k = 4 c .. 4 c + 3) of row x in a
+// [128 x][32 k] fp32 tile (x-major, the layout of an operand whose k axis is
+// contiguous in memory).
+__device__ __forceinline__ uint32_t xk_off(uint32_t x, uint32_t c) {
+  return x * 128u + ((c ^ ((x >> 1) & 7u)) << 4);
 }
 
 // Tile modes: kGrid (every tile whole), kEdge (chunks of 4 floats past the
@@ -90,12 +101,10 @@ __device__ __forceinline__ void store_tile32(uint8_t* lds, const u32x4 v[4]) {
     for (int i = 0; i < 4; ++i)
       *reinterpret_cast<u32x4*>(lds + swz32(t / 32 + 8 * i, (t % 32) * 4)) = v[i];
   } else {
-    // v[j] = x row (t/8)*4 + j, k = (t%8)*4 .. +3 ; w[i] = k row (t%8)*4 + i.
-    u32x4 w[4];
-    transpose4x4_u32(v, w);
+    // v[j] = x row (t/8)*4 + j, k chunk t%8: stored as loaded.
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(lds + swz32((t % 8) * 4 + i, (t / 8) * 4)) = w[i];
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4*>(lds + xk_off((t / 8) * 4 + j, t % 8)) = v[j];
   }
 }
 
@@ -158,19 +167,36 @@ __global__ __launch_bounds__(kThreads, 3) void gemm_f32_128_kernel(
     }
     const uint8_t* la = smem;
     const uint8_t* lb = smem + kTileBytes;
+    // The k pair of substep p is (p, 16 + p) for lanes 0-31 and 32-63 (a
+    // permutation of the step's 32 k that A and B share): in an x-major
+    // tile a lane's values for 4 consecutive substeps are one 16-byte chunk
+    // of its row; a k-major tile is read one element per substep.
+    const uint32_t g = lane / 32;
+    auto frag4 = [&]<bool XContig>(const uint8_t* l, uint32_t x, uint32_t q) __attribute__((always_inline)) {
+      if constexpr (XContig) {
+        u32x4 v;
 #pragma unroll
-    for (uint32_t p = 0; p < kBK / 2; ++p) {
-      const uint32_t k = 2 * p + lane / 32;
-      float fa[2], fb[2];
+        for (int w = 0; w < 4; ++w) v[w] = __float_as_uint(read32(l, 16 * g + 4 * q + w, x));
+        return v;
+      } else {
+        return *reinterpret_cast<const u32x4*>(l + xk_off(x, 4 * g + q));
+      }
+    };
 #pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = read32(la, k, wm + 32 * i + lane % 32);
+    for (uint32_t q = 0; q < kBK / 8; ++q) {
+      u32x4 fa[2], fb[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = read32(lb, k, wn + 32 * j + lane % 32);
+      for (int i = 0; i < 2; ++i) fa[i] = frag4.template operator()<kAX>(la, wm + 32 * i + lane % 32, q);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 2; ++j) fb[j] = frag4.template operator()<kBX>(lb, wn + 32 * j + lane % 32, q);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j], fa[i], acc[i][j], 0, 0, 0);
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(fb[j][w]),
+                                                            __uint_as_float(fa[i][w]), acc[i][j], 0, 0, 0);
     }
     if (more) {
       __syncthreads();  // every wave is done reading this tile
