@@ -960,6 +960,10 @@ int launch_attention_f16(hipStream_t stream, const AttentionArgs& a) {
                        ((uintptr_t)a.value % 16 == 0) && ((uintptr_t)a.out % 16 == 0);
   for (int i = 0; i < 3; ++i)
     if (a.heads[i] == 0 || a.streams % a.heads[i] != 0) return IPUS_ERROR_INVALID_ARGUMENT;
+  // Every kernel holds a row pitch (heads x width elements) in 32 bits.
+  if ((uint64_t)a.heads[0] * a.width > 0xffffffffull || (uint64_t)a.heads[1] * a.width > 0xffffffffull ||
+      (uint64_t)a.heads[2] * a.value_width > 0xffffffffull)
+    return IPUS_ERROR_INVALID_ARGUMENT;
   // The fast kernel addresses one stream's K or V through a buffer
   // descriptor with a 31-bit byte range; the offsets of the last block's
   // rows (up to 63 past the end) and of padding chunks stay below 2^32.
