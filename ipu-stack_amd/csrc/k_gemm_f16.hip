@@ -42,7 +42,8 @@
 //   * the MFMA computes tiles of C^T (B fragment as the first operand) so
 //     each lane holds 4 consecutive columns of one row of C; the epilogue
 //     stages each wave's 128 x 128 result in LDS and writes 256-byte row
-//     runs with streaming stores;
+//     runs with streaming stores (cached stores for a GELU result, which the
+//     next GEMM of an MLP reads);
 //   * block ids are remapped so that the blocks one XCD runs (round-robin
 //     dispatch over 8 XCDs) form a compact group of C tiles sharing L2;
 //   * partial tiles: rows of a K-contiguous operand past M or N lie past
@@ -50,7 +51,8 @@
 //     and (in the KTail instantiation, K % 64 != 0) K-contiguous chunks and
 //     MN-contiguous rows past K on the last step, get an offset past the
 //     range; the epilogue stores only rows < M and 8-column chunks < N.
-// General kernel: 64 x 64 tiles, bounds-checked scalar loads, any shape.
+// Small-tile kernel (64 x 64 or 32 x 32 tiles): shapes with few 256 x 256
+// tiles, and any shape or alignment the fast kernel does not take.
 #include "../../include/ipus.h"
 
 #include <mutex>
@@ -909,8 +911,11 @@ int launch_gemm_f16_split_noalloc(hipStream_t stream, int device, const GemmArgs
     if (device >= 0 && device < kMaxScratchDevices) parts = g_scratch_ptr[device];
   }
   if (!parts) return IPUS_ERROR_NO_DEVICE;
-  const uint64_t count = (uint64_t)a.batches * a.rows * a.columns;
-  if (splits == 0 || count * splits > IPUS_SPLIT_SCRATCH_BYTES / sizeof(float))
+  uint64_t count = 0, total = 0;
+  if (splits == 0 || __builtin_mul_overflow((uint64_t)a.batches, (uint64_t)a.rows, &count) ||
+      __builtin_mul_overflow(count, (uint64_t)a.columns, &count) ||
+      __builtin_mul_overflow(count, (uint64_t)splits, &total) ||
+      total > IPUS_SPLIT_SCRATCH_BYTES / sizeof(float))
     return IPUS_ERROR_UNSUPPORTED_COUNT;
   GemmArgs s = a;
   s.out = parts;

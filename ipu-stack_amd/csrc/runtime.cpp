@@ -985,11 +985,17 @@ extern "C" int ipus_gemm_f16_split_noalloc(ipus_context* ctx, void* output, cons
   if (!ctx || !output || !left || !right) return fail(IPUS_ERROR_INVALID_ARGUMENT, "null argument");
   if (batches > 65535 || splits == 0 || splits > 64)
     return fail(IPUS_ERROR_INVALID_ARGUMENT, "batches must be <= 65535 and splits in 1..64");
-  const uint64_t need = (uint64_t)batches * rows * columns * splits * sizeof(float);
-  if (need > IPUS_SPLIT_SCRATCH_BYTES)
+  // batches x rows x columns can pass 2^64 bytes: an overflowing product
+  // must not slip under the limit.
+  uint64_t need = 0;
+  const bool over = __builtin_mul_overflow((uint64_t)batches, (uint64_t)rows, &need) ||
+                    __builtin_mul_overflow(need, (uint64_t)columns, &need) ||
+                    __builtin_mul_overflow(need, (uint64_t)splits * sizeof(float), &need);
+  if (over || need > IPUS_SPLIT_SCRATCH_BYTES)
     return fail(IPUS_ERROR_UNSUPPORTED_COUNT,
                 "split-K partials need %llu bytes; the no-allocation scratch holds %llu",
-                (unsigned long long)need, (unsigned long long)IPUS_SPLIT_SCRATCH_BYTES);
+                over ? ~0ull : (unsigned long long)need,
+                (unsigned long long)IPUS_SPLIT_SCRATCH_BYTES);
   if (int e = use_device(ctx)) return e;
   GemmArgs a;
   a.out = output;

@@ -58,3 +58,13 @@ def test_no_alloc_split_k_rejects_partials_beyond_the_scratch(ipus, ctx):
         ctx.gemm_f16_split_noalloc(out, out, out, 1, 2048, 2048, 4096, splits=2)
     assert err.value.status == ipus.ERROR_UNSUPPORTED_COUNT and "scratch" in err.value.message
     out.free()
+
+
+def test_no_alloc_split_k_rejects_a_size_product_past_64_bits(ipus, ctx):
+    out = ctx.alloc(64)
+    # 2^31 x 2^31 fp32 partials are 2^64 bytes: the size product wraps to 0
+    # in 64 bits and must still be refused before any launch.
+    with pytest.raises(ipus.IpusError) as err:
+        ctx.gemm_f16_split_noalloc(out, out, out, 1, 1 << 31, 1 << 31, 64, splits=1)
+    assert err.value.status == ipus.ERROR_UNSUPPORTED_COUNT and "scratch" in err.value.message
+    out.free()
