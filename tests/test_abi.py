@@ -35,8 +35,9 @@ def test_python_binding_covers_every_declared_symbol(ipus):
 
 
 def test_rust_binding_block_covers_every_declared_symbol():
-    """INTEGRATION.md's extern "C" block (what a Rust caller links against)
-    declares every entry point of include/*.h and nothing else."""
+    """The integration guide's Rust extern "C" block (what a Rust caller
+    links against) declares every entry point of include/*.h and nothing
+    else."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     rust = set(re.findall(r"pub fn (ipus_[a-z0-9_]+)\(", text))
     assert rust == declared_functions()
